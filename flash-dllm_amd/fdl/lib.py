@@ -1,0 +1,125 @@
+"""ctypes binding of libfdl.so, the C ABI declared in include/fdl.h.
+
+torch is imported first so that its HIP runtime (libamdhip64.so.7) is already loaded when
+libfdl.so is opened: the dynamic loader then binds libfdl.so to that same runtime, and the
+streams and device pointers torch hands out are valid inside the library.
+
+There is no fallback: if libfdl.so is missing, every entry point raises FdlError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime libfdl.so must share)
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libfdl.so"
+
+# status codes (include/fdl.h)
+FDL_OK = 0
+FDL_ERR_NULL = -1
+FDL_ERR_SHAPE = -2
+FDL_ERR_RANGE = -3
+FDL_ERR_UNSUPPORTED = -4
+FDL_ERR_HIP = -5
+
+IMP_NONE = 0
+IMP_RAW_LOGIT = 1
+IMP_SOFTMAX_COLSUM = 2
+
+_STATUS_NAMES = {
+    FDL_ERR_NULL: "FDL_ERR_NULL",
+    FDL_ERR_SHAPE: "FDL_ERR_SHAPE",
+    FDL_ERR_RANGE: "FDL_ERR_RANGE",
+    FDL_ERR_UNSUPPORTED: "FDL_ERR_UNSUPPORTED",
+    FDL_ERR_HIP: "FDL_ERR_HIP",
+}
+
+
+class FdlError(RuntimeError):
+    """A C-ABI call returned a non-zero status (or the library is missing)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes), in declaration order of include/fdl.h
+SIGNATURES: dict[str, tuple] = {
+    "fdl_last_error": (ctypes.c_char_p, []),
+    "fdl_abi_version": (ctypes.c_int, []),
+    "fdl_qkv_rope_cache": (ctypes.c_int, [
+        _p, _p, _p, _p,          # x, wq, wk, wv
+        _p, _p, _i64,            # rope_sin, rope_cos, n_rope_rows
+        _p, _p, _i64,            # slot, rope_row, n_rows
+        _i64, _i64, _i64,        # d_model, n_heads, head_dim
+        _p, _p, _p, _i64, _i32,  # q_out, k_out, v_out, n_kv_rows, kv_packed
+        _p,                      # stream
+    ]),
+    "fdl_block_attention": (ctypes.c_int, [
+        _p, _p, _p,                   # q, k_cache, v_cache
+        _i64, _i64, _i64, _i64, _i64,  # n_q_rows, n_slots, d_model, n_heads, head_dim
+        _p, _i64, _i64, _i32,         # page_table, n_seq, max_pages, page_log2
+        _p, _i64, _p, _i64,           # work, n_work, row_idx, n_row_idx
+        _f32, _p, _i32, _p,           # softmax_scale, out, imp_mode, imp_part
+        _p,                           # stream
+    ]),
+    "fdl_importance_accumulate": (ctypes.c_int, [
+        _p, _i64, _i64,               # imp_part, n_heads, n_slots
+        _p, _i64, _i64, _i32,         # page_table, n_seq, max_pages, page_log2
+        _p, _i64, _f32, _p,           # work, n_work, scale, scores
+        _p,                           # stream
+    ]),
+    "fdl_importance_rank": (ctypes.c_int, [
+        _p, _i64, _p, _i64,           # scores, n_scores, slots, n_slot_entries
+        _p, _i64, _i32,               # seg, n_seg, max_len
+        _p, _i32, _p,                 # topk_out, k, stream
+    ]),
+    "fdl_verify_attention": (ctypes.c_int, [
+        _p, _p, _p, _p, _p,           # q, k_blk, v_blk, k_cache, v_cache
+        _i64, _i64, _i64, _i64, _i64,  # n_q_rows, n_slots, d_model, n_heads, head_dim
+        _p, _i64, _p, _i64,           # key_slots, n_keys, vblocks, n_vblocks
+        _p, _i32, _f32, _p, _p,       # mask, block_rows, softmax_scale, out, stream
+    ]),
+    "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),
+    "fdl_validate_work": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i64]),
+    "fdl_validate_vblocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i32]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Opens libfdl.so once; raises FdlError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("FDL_LIBRARY", LIB_PATH))
+    if not path.exists():
+        raise FdlError(FDL_ERR_UNSUPPORTED,
+                       f"{path} not found: build it with `python flash-dllm_amd/build.py` "
+                       "(there is no non-HIP fallback)")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.fdl_abi_version() != 1:
+        raise FdlError(FDL_ERR_UNSUPPORTED, f"{path}: ABI version {lib.fdl_abi_version()} != 1")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Calls entry point `name`; raises FdlError with the library's message on failure."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != FDL_OK:
+        msg = lib.fdl_last_error().decode(errors="replace")
+        raise FdlError(status, msg or name)

@@ -1,0 +1,176 @@
+"""torch-facing wrappers of the C-ABI entry points (include/fdl.h).
+
+Each wrapper checks devices, dtypes, shapes and contiguity, then calls the library on
+torch's current HIP stream of the tensors' device. The calls are asynchronous, like the
+reference's Triton launches. There is no CPU or PyTorch fallback: a tensor that is not on
+a GPU is an error.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import lib as _lib
+from .schedule import AttnPlan
+
+BF16 = torch.bfloat16
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = None,
+          device: torch.device | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise _lib.FdlError(_lib.FDL_ERR_UNSUPPORTED,
+                            f"{name} is on {t.device}; the HIP path needs GPU tensors")
+    if device is not None and t.device != device:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} has dtype {t.dtype}, expected {dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} has {t.dim()} dims, expected {ndim}")
+    if not t.is_contiguous():
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} must be contiguous")
+
+
+def qkv_rope_cache(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor,
+                   rope_sin: torch.Tensor, rope_cos: torch.Tensor, slot: torch.Tensor,
+                   q_out: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor, n_heads: int,
+                   rope_row: torch.Tensor | None = None, kv_packed: bool = False) -> None:
+    """Fused QKV projection + RoPE + K/V write (fdl_qkv_rope_cache).
+
+    x [Q, D] bf16; w* [D, D] bf16; rope tables fp32 [R, hd]; slot int64 [Q];
+    q_out [Q, D]; k_out/v_out the cache [n_slots, D] (or [Q, D] with kv_packed).
+    """
+    dev = x.device
+    _need(x, "x", BF16, 2)
+    n_rows, d_model = x.shape
+    for n, t in (("wq", wq), ("wk", wk), ("wv", wv)):
+        _need(t, n, BF16, 2, dev)
+        if tuple(t.shape) != (d_model, d_model):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{n} has shape {tuple(t.shape)}, expected ({d_model}, {d_model})")
+    _need(rope_sin, "rope_sin", torch.float32, 2, dev)
+    _need(rope_cos, "rope_cos", torch.float32, 2, dev)
+    if rope_sin.shape != rope_cos.shape:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "rope_sin and rope_cos differ in shape")
+    head_dim = d_model // n_heads
+    if rope_sin.shape[1] != head_dim:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"rope tables have {rope_sin.shape[1]} columns, expected {head_dim}")
+    _need(slot, "slot", torch.int64, 1, dev)
+    if slot.shape[0] != n_rows:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"slot has {slot.shape[0]} entries for {n_rows} rows")
+    if rope_row is not None:
+        _need(rope_row, "rope_row", torch.int64, 1, dev)
+        if rope_row.shape[0] != n_rows:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "rope_row length differs from the row count")
+    _need(q_out, "q_out", BF16, 2, dev)
+    if tuple(q_out.shape) != (n_rows, d_model):
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "q_out shape differs from x")
+    _need(k_out, "k_out", BF16, 2, dev)
+    _need(v_out, "v_out", BF16, 2, dev)
+    if k_out.shape != v_out.shape or k_out.shape[1] != d_model:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "k_out/v_out must both be [n, d_model]")
+    _lib.call("fdl_qkv_rope_cache", x.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
+              rope_sin.data_ptr(), rope_cos.data_ptr(), rope_sin.shape[0],
+              slot.data_ptr(), _ptr(rope_row), n_rows, d_model, n_heads, head_dim,
+              q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), k_out.shape[0],
+              1 if kv_packed else 0, _stream(x))
+
+
+def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    plan: AttnPlan, out: torch.Tensor, n_heads: int, softmax_scale: float,
+                    imp_mode: int = _lib.IMP_NONE, imp_part: torch.Tensor | None = None) -> None:
+    """Block-table attention with the importance side output (fdl_block_attention)."""
+    dev = q.device
+    _need(q, "q", BF16, 2)
+    _need(k_cache, "k_cache", BF16, 2, dev)
+    _need(v_cache, "v_cache", BF16, 2, dev)
+    _need(out, "out", BF16, 2, dev)
+    if k_cache.shape != v_cache.shape or k_cache.shape[1] != q.shape[1] or out.shape != q.shape:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "q/out/k_cache/v_cache shapes disagree")
+    if plan.work_d is None:
+        plan.to(dev)
+    if imp_mode != _lib.IMP_NONE:
+        if imp_part is None:
+            raise _lib.FdlError(_lib.FDL_ERR_NULL, "imp_part is required with an importance mode")
+        _need(imp_part, "imp_part", torch.float32, 2, dev)
+        if tuple(imp_part.shape) != (n_heads, k_cache.shape[0]):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "imp_part must be [n_heads, n_slots]")
+    d_model = q.shape[1]
+    _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              q.shape[0], k_cache.shape[0], d_model, n_heads, d_model // n_heads,
+              plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
+              plan.page_log2, plan.work_d.data_ptr(), plan.n_work, plan.row_idx_d.data_ptr(),
+              max(int(plan.row_idx.size), 1), float(softmax_scale), out.data_ptr(), int(imp_mode),
+              _ptr(imp_part), _stream(q))
+
+
+def importance_accumulate(imp_part: torch.Tensor, plan: AttnPlan, scale: float,
+                          scores: torch.Tensor) -> None:
+    """scores[slot] += scale * sum_h imp_part[h][slot] (fdl_importance_accumulate)."""
+    dev = imp_part.device
+    _need(imp_part, "imp_part", torch.float32, 2)
+    _need(scores, "scores", torch.float32, 1, dev)
+    if scores.shape[0] != imp_part.shape[1]:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "scores length differs from imp_part columns")
+    if plan.work_d is None:
+        plan.to(dev)
+    _lib.call("fdl_importance_accumulate", imp_part.data_ptr(), imp_part.shape[0], imp_part.shape[1],
+              plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
+              plan.page_log2, plan.work_d.data_ptr(), plan.n_work, float(scale), scores.data_ptr(),
+              _stream(imp_part))
+
+
+def importance_rank(scores: torch.Tensor, slots: torch.Tensor, seg: torch.Tensor, max_len: int,
+                    topk_out: torch.Tensor | None = None, k: int = 0) -> None:
+    """Sorts each segment (start, len) of `slots` in place by importance and gathers the
+    top-k (fdl_importance_rank)."""
+    dev = scores.device
+    _need(scores, "scores", torch.float32, 1)
+    _need(slots, "slots", torch.int64, None, dev)
+    _need(seg, "seg", torch.int32, 2, dev)
+    if seg.shape[1] != 2:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "seg must be [n_seg, 2]")
+    if topk_out is not None:
+        _need(topk_out, "topk_out", torch.int64, 2, dev)
+        if tuple(topk_out.shape) != (seg.shape[0], k):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "topk_out must be [n_seg, k]")
+    _lib.call("fdl_importance_rank", scores.data_ptr(), scores.shape[0], slots.data_ptr(),
+              slots.numel(), seg.data_ptr(), seg.shape[0], int(max_len), _ptr(topk_out),
+              int(k if topk_out is not None else 0), _stream(scores))
+
+
+def verify_attention(q: torch.Tensor, k_blk: torch.Tensor, v_blk: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, key_slots: torch.Tensor,
+                     vblocks: torch.Tensor, mask: torch.Tensor, block_rows: int,
+                     out: torch.Tensor, n_heads: int, softmax_scale: float) -> None:
+    """Flash-Verify attention (fdl_verify_attention)."""
+    dev = q.device
+    _need(q, "q", BF16, 2)
+    for n, t in (("k_blk", k_blk), ("v_blk", v_blk), ("out", out)):
+        _need(t, n, BF16, 2, dev)
+        if t.shape != q.shape:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{n} shape differs from q")
+    _need(k_cache, "k_cache", BF16, 2, dev)
+    _need(v_cache, "v_cache", BF16, 2, dev)
+    _need(key_slots, "key_slots", torch.int64, 1, dev)
+    _need(vblocks, "vblocks", torch.int32, 2, dev)
+    if mask.dtype == torch.bool:
+        mask = mask.view(torch.uint8)
+    _need(mask, "mask", torch.uint8, 2, dev)
+    nv = vblocks.shape[0]
+    if tuple(mask.shape) != (nv * block_rows, block_rows):
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"mask must be [{nv * block_rows}, {block_rows}]")
+    d_model = q.shape[1]
+    _lib.call("fdl_verify_attention", q.data_ptr(), k_blk.data_ptr(), v_blk.data_ptr(),
+              k_cache.data_ptr(), v_cache.data_ptr(), q.shape[0], k_cache.shape[0], d_model,
+              n_heads, d_model // n_heads, key_slots.data_ptr() if key_slots.numel() else None,
+              key_slots.numel(), vblocks.data_ptr(), nv, mask.data_ptr(), int(block_rows),
+              float(softmax_scale), out.data_ptr(), _stream(q))

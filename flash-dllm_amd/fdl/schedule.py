@@ -1,0 +1,154 @@
+"""Host-side schedule building for the block-table attention.
+
+The reference launches masked-block attention and tracked-block attention separately
+(flash_cache_triton.py:561-607), so every sequence's K/V are streamed twice. Here a
+sequence's masked rows and tracked rows are packed into the same tiles (up to 64 query
+rows per tile): masked rows first, so that the first `n_imp` rows of the sequence's first
+tile are the rows whose logits feed the importance scores (flash_cache_triton.py:155-158,
+:614-615).
+
+Work items (int32 x 8, see include/fdl.h):
+    (batch, k_begin, k_end, row_off, n_rows, n_imp, 0, 0)
+Tiles are issued longest-first (keys x row groups), so that the long full-recompute tiles
+start before the short ones.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+MAX_TILE_ROWS = 64
+DEFAULT_PAGE_LOG2 = 5  # 32-slot pages
+
+
+@dataclass
+class SeqRows:
+    """The query rows of one sequence in one attention launch."""
+    batch: int           # page-table row
+    k_end: int           # keys [k_begin, k_end)
+    rows: np.ndarray     # packed query-row indices, importance rows first
+    n_imp: int = 0       # leading rows that feed the importance scores
+    k_begin: int = 0
+
+
+def contiguous_page_table(n_seq: int, max_length: int, page_log2: int = DEFAULT_PAGE_LOG2) -> np.ndarray:
+    """The reference layout (slot = b * L + n, llada/generate.py:178-180) as a page table."""
+    page = 1 << page_log2
+    if max_length % page:
+        raise ValueError(f"max_length {max_length} is not a multiple of the page size {page}")
+    per = max_length // page
+    return (np.arange(n_seq, dtype=np.int64)[:, None] * per + np.arange(per)[None, :]).astype(np.int32)
+
+
+def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS) -> tuple[np.ndarray, np.ndarray]:
+    """Splits each sequence's rows into tiles of at most `max_rows` rows.
+
+    Returns (work int32 [n, 8], row_idx int32). The importance rows of a sequence must fit
+    in its first tile.
+    """
+    items = []
+    row_chunks = []
+    off = 0
+    for sq in seqs:
+        rows = np.asarray(sq.rows, dtype=np.int32).reshape(-1)
+        if sq.n_imp > max_rows:
+            raise ValueError(f"{sq.n_imp} importance rows do not fit one {max_rows}-row tile")
+        if sq.n_imp > len(rows):
+            raise ValueError("n_imp exceeds the number of rows")
+        for t0 in range(0, len(rows), max_rows):
+            chunk = rows[t0:t0 + max_rows]
+            n_imp = sq.n_imp if t0 == 0 else 0
+            items.append((sq.batch, sq.k_begin, sq.k_end, off, len(chunk), n_imp, 0, 0))
+            row_chunks.append(chunk)
+            off += len(chunk)
+    if not items:
+        return np.zeros((0, 8), dtype=np.int32), np.zeros(0, dtype=np.int32)
+    work = np.asarray(items, dtype=np.int32)
+    row_idx = np.concatenate(row_chunks).astype(np.int32)
+    # longest first: keys x 16-row groups
+    cost = (work[:, 2].astype(np.int64) - work[:, 1]) * ((work[:, 4].astype(np.int64) + 15) // 16)
+    order = np.argsort(-cost, kind="stable")
+    return np.ascontiguousarray(work[order]), row_idx
+
+
+def seqs_from_reference_blocks(masked_blocks: np.ndarray, tracked_blocks: np.ndarray,
+                               importance: bool) -> list[SeqRows]:
+    """Groups the reference's block tables (rows (batch, k_end, q0, q1),
+    llada/generate.py:52-58, :146-163, :439-465) by sequence: masked rows first, then
+    tracked rows. With `importance`, the masked rows are the importance rows."""
+    masked_blocks = np.asarray(masked_blocks, dtype=np.int64).reshape(-1, 4)
+    tracked_blocks = np.asarray(tracked_blocks, dtype=np.int64).reshape(-1, 4)
+    by_key: dict[tuple[int, int], list[list[np.ndarray]]] = {}
+    order: list[tuple[int, int]] = []
+    for kind, table in ((0, masked_blocks), (1, tracked_blocks)):
+        for b, k_end, q0, q1 in table:
+            key = (int(b), int(k_end))
+            if key not in by_key:
+                by_key[key] = [[], []]
+                order.append(key)
+            by_key[key][kind].append(np.arange(q0, q1, dtype=np.int32))
+    seqs = []
+    for key in order:
+        m, t = by_key[key]
+        m_rows = np.concatenate(m) if m else np.zeros(0, np.int32)
+        t_rows = np.concatenate(t) if t else np.zeros(0, np.int32)
+        seqs.append(SeqRows(batch=key[0], k_end=key[1], rows=np.concatenate([m_rows, t_rows]),
+                            n_imp=len(m_rows) if importance else 0))
+    return seqs
+
+
+@dataclass
+class AttnPlan:
+    """A ready-to-launch attention schedule: host tables and their device copies."""
+    work: np.ndarray
+    row_idx: np.ndarray
+    page_table: np.ndarray
+    page_log2: int
+    work_d: torch.Tensor = field(repr=False, default=None)
+    row_idx_d: torch.Tensor = field(repr=False, default=None)
+    page_table_d: torch.Tensor = field(repr=False, default=None)
+
+    @property
+    def n_work(self) -> int:
+        return int(self.work.shape[0])
+
+    @property
+    def has_importance(self) -> bool:
+        return bool(self.n_work and (self.work[:, 5] > 0).any())
+
+    def to(self, device) -> "AttnPlan":
+        """Copies the tables to `device` (one packed host->device copy)."""
+        parts = [self.work.reshape(-1), self.row_idx.reshape(-1), self.page_table.reshape(-1)]
+        flat = torch.from_numpy(np.concatenate(parts).astype(np.int32))
+        if torch.device(device).type == "cuda":
+            flat = flat.pin_memory()
+        flat = flat.to(device, non_blocking=True)
+        a = parts[0].size
+        b = a + parts[1].size
+        self.work_d = flat[:a].view(-1, 8)
+        self.row_idx_d = flat[a:b]
+        self.page_table_d = flat[b:].view(self.page_table.shape)
+        return self
+
+    def validate(self, n_q_rows: int, n_slots: int) -> None:
+        """Runs the C-ABI host validator on the host tables (raises FdlError)."""
+        from . import lib as _lib
+        w = np.ascontiguousarray(self.work, dtype=np.int32)
+        r = np.ascontiguousarray(self.row_idx, dtype=np.int32)
+        if r.size == 0:
+            r = np.zeros(1, np.int32)
+        p = np.ascontiguousarray(self.page_table, dtype=np.int32)
+        _lib.call("fdl_validate_work", w.ctypes.data, w.shape[0], r.ctypes.data, self.row_idx.size,
+                  n_q_rows, p.ctypes.data, p.shape[0], p.shape[1], self.page_log2, n_slots)
+
+
+def make_plan(seqs: list[SeqRows], page_table: np.ndarray, page_log2: int = DEFAULT_PAGE_LOG2,
+              device=None, max_rows: int = MAX_TILE_ROWS) -> AttnPlan:
+    work, row_idx = build_work(seqs, max_rows)
+    plan = AttnPlan(work=work, row_idx=row_idx, page_table=np.ascontiguousarray(page_table, dtype=np.int32),
+                    page_log2=page_log2)
+    if device is not None:
+        plan.to(device)
+    return plan

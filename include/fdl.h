@@ -1,0 +1,188 @@
+/*
+ * fdl.h -- C ABI of the MI355X (gfx950) Flash-Cache hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream (passed as
+ * `void*`, i.e. a hipStream_t; NULL means the null stream). Entry points validate their
+ * scalar arguments on the host, enqueue kernels on the stream and return without
+ * synchronising. Status: 0 on success, a negative FDL_ERR_* code otherwise; the text of
+ * the last error of the calling thread is returned by fdl_last_error().
+ *
+ * Buffers are caller-owned. bf16 means IEEE bfloat16 stored as uint16. Row-major
+ * everywhere. d_model = n_heads * head_dim; only head_dim == 128 is implemented.
+ *
+ * Table formats
+ *   work item (int32 x 8), one per attention tile:
+ *     [0] batch     row of the page table holding this sequence's pages
+ *     [1] k_begin   first logical key position (inclusive)
+ *     [2] k_end     last logical key position (exclusive), the reference's seqlen_k
+ *     [3] row_off   offset into row_idx of this tile's query rows
+ *     [4] n_rows    number of query rows (1..64)
+ *     [5] n_imp     the first n_imp rows of the tile feed the importance scores
+ *     [6] reserved  (0)
+ *     [7] reserved  (0)
+ *   page table (int32 [n_seq][max_pages]): logical key n of sequence b lives in cache
+ *     slot page_table[b][n >> page_log2] * (1 << page_log2) + (n & ((1 << page_log2) - 1)).
+ *     The reference's contiguous layout (slot = b*L + n) is the page table
+ *     page_table[b][p] = b*L/P + p.
+ *   verify block (int32 x 4): (k0, k1, q0, q1) exactly as the reference's verify block
+ *     table: keys key_slots[k0..k1) from the cache, query rows [q0, q1) which are also
+ *     the in-block keys.
+ */
+#ifndef FDL_H_
+#define FDL_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FDL_ABI_VERSION 1
+
+enum fdl_status {
+  FDL_OK = 0,
+  FDL_ERR_NULL = -1,        /* a required pointer is NULL */
+  FDL_ERR_SHAPE = -2,       /* inconsistent or unsupported dimensions */
+  FDL_ERR_RANGE = -3,       /* a table entry lies outside the buffer it indexes */
+  FDL_ERR_UNSUPPORTED = -4, /* a valid request that the kernels do not implement */
+  FDL_ERR_HIP = -5,         /* a HIP runtime call failed */
+};
+
+enum fdl_importance_mode {
+  FDL_IMP_NONE = 0,
+  /* sum over importance rows of the raw, unscaled logit q.k (flash_cache_triton.py:155-158) */
+  FDL_IMP_RAW_LOGIT = 1,
+  /* sum over importance rows of softmax(scale * q.k) probabilities (column sums) */
+  FDL_IMP_SOFTMAX_COLSUM = 2,
+};
+
+/* Text of the calling thread's last error ("" if none). */
+const char* fdl_last_error(void);
+
+/* FDL_ABI_VERSION of the library. */
+int fdl_abi_version(void);
+
+/*
+ * Fused QKV projection + rotate-half RoPE + K/V write.
+ * Replaces the launches of _flash_qkv_proj_cache_fwd (flash_cache_triton.py:15-100,
+ * launched at :541-559) and, with kv_packed = 1, _flash_verify_qkv_proj_fwd
+ * (flash_cache_triton.py:255-338, launched at :505-519).
+ *
+ *   x        bf16 [n_rows][d_model]         normalised hidden states (x_normed)
+ *   wq/wk/wv bf16 [d_model][d_model]        nn.Linear weights, [out][in]
+ *   rope_sin, rope_cos fp32 [n_rope_rows][head_dim]
+ *   slot     int64 [n_rows]  cache slot of each row (the reference's query_pos_flat)
+ *   rope_row int64 [n_rows]  row of the sin/cos tables for each row; NULL = use slot
+ *   q_out    bf16 [n_rows][d_model]         rotated Q, packed by row
+ *   k_out/v_out bf16: kv_packed == 0 -> cache [n_kv_rows][d_model], row slot[r] is
+ *            overwritten with the rotated K / V of row r; kv_packed == 1 -> packed
+ *            [n_rows][d_model] (n_kv_rows must equal n_rows).
+ * Rows whose slot or rope_row is out of range are skipped by the kernel; use
+ * fdl_validate_rows to reject them on the host.
+ */
+int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void* wv,
+                       const float* rope_sin, const float* rope_cos, int64_t n_rope_rows,
+                       const int64_t* slot, const int64_t* rope_row, int64_t n_rows,
+                       int64_t d_model, int64_t n_heads, int64_t head_dim, void* q_out,
+                       void* k_out, void* v_out, int64_t n_kv_rows, int32_t kv_packed,
+                       void* stream);
+
+/*
+ * Block-table attention over the KV cache for variable per-sequence query lengths, with
+ * the importance side output.
+ * Replaces _flash_masked_attention_fwd (flash_cache_triton.py:103-177, launched at
+ * :561-577) and _flash_tracked_attention_fwd (:180-252, launched at :589-607) in one
+ * launch: a tile may hold the masked rows and the tracked rows of one sequence, so the
+ * sequence's K/V are streamed once. Bidirectional (no causal mask).
+ *
+ *   q        bf16 [n_q_rows][d_model]       rotated queries (q_out of fdl_qkv_rope_cache)
+ *   k_cache, v_cache bf16 [n_slots][d_model]
+ *   page_table int32 [n_seq][max_pages]; page size 1 << page_log2 (4 <= page_log2 <= 12)
+ *   work     int32 [n_work][8] (see above); row_idx int32 [n_row_idx]
+ *   out      bf16 [n_q_rows][d_model]       rows named by row_idx are written
+ *   imp_mode FDL_IMP_*; imp_part fp32 [n_heads][n_slots]: for every tile with n_imp > 0,
+ *            imp_part[h][slot(n)] = sum over its first n_imp rows r of the head-h term
+ *            (raw: q_r.k_n; softmax: exp(scale*q_r.k_n - lse_r)), for n in [k_begin, k_end).
+ *            Slots of other tiles are left untouched. Reduce over heads with
+ *            fdl_importance_accumulate. Each sequence must have at most one tile with
+ *            n_imp > 0.
+ */
+int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
+                        int64_t n_q_rows, int64_t n_slots, int64_t d_model, int64_t n_heads,
+                        int64_t head_dim, const int32_t* page_table, int64_t n_seq,
+                        int64_t max_pages, int32_t page_log2, const int32_t* work,
+                        int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
+                        float softmax_scale, void* out, int32_t imp_mode, float* imp_part,
+                        void* stream);
+
+/*
+ * scores[slot(n)] += scale * sum_{h = 0..n_heads-1} imp_part[h][slot(n)] for every tile
+ * with n_imp > 0 and n in [k_begin, k_end), heads summed in ascending order.
+ * Replaces `attn_scores += S.mean((0, 1)).view(-1)` (flash_cache_triton.py:614-615) with
+ * scale = 1 / (block_m * n_heads).
+ */
+int fdl_importance_accumulate(const float* imp_part, int64_t n_heads, int64_t n_slots,
+                              const int32_t* page_table, int64_t n_seq, int64_t max_pages,
+                              int32_t page_log2, const int32_t* work, int64_t n_work,
+                              float scale, float* scores, void* stream);
+
+/*
+ * Importance ranking of decoded slots (generate.py:364-366) and top-k gather (the
+ * tracked refresh set, generate.py:375-381).
+ *   scores fp32 [n_scores] indexed by slot
+ *   slots  int64, segments seg[i] = (start, len) int32 [n_seg][2]: on return each segment
+ *          slots[start .. start+len) is sorted ascending by (score, then slot descending),
+ *          the reference's ascending sort with ties resolved so that among equal scores the
+ *          lower slot ranks higher.
+ *   topk_out int64 [n_seg][k] or NULL: the k highest-ranked slots of each segment, in rank
+ *          order (score descending, slot ascending), -1 where a segment is shorter than k.
+ *   max_len  upper bound of every len (<= 8192).
+ */
+int fdl_importance_rank(const float* scores, int64_t n_scores, int64_t* slots,
+                        int64_t n_slot_entries, const int32_t* seg, int64_t n_seg,
+                        int32_t max_len, int64_t* topk_out, int32_t k, void* stream);
+
+/*
+ * Flash-Verify attention. Replaces _flash_verify_attention_fwd (flash_cache_triton.py:
+ * 341-428, launched at :523-535): for each verify block (k0, k1, q0, q1) and head, the
+ * rows [q0, q1) attend to the cache keys key_slots[k0..k1) and to the block's own rows
+ * as in-block keys (k_blk/v_blk, packed by row) under the block's boolean mask.
+ *   q, k_blk, v_blk bf16 [n_q_rows][d_model]    (outputs of fdl_qkv_rope_cache, kv_packed=1)
+ *   key_slots int64 [n_keys]
+ *   vblocks  int32 [n_vblocks][4]; q1 - q0 <= block_rows <= 64
+ *   mask     uint8 [n_vblocks * block_rows][block_rows]; row i of block v is
+ *            mask[v*block_rows + i]; nonzero = may attend. Column j is additionally
+ *            valid only if q0 + j < q1.
+ *   out      bf16 [n_q_rows][d_model]
+ * Softmax is exact over the union of both key sets (the running maximum includes the
+ * in-block logits).
+ */
+int fdl_verify_attention(const void* q, const void* k_blk, const void* v_blk,
+                         const void* k_cache, const void* v_cache, int64_t n_q_rows,
+                         int64_t n_slots, int64_t d_model, int64_t n_heads, int64_t head_dim,
+                         const int64_t* key_slots, int64_t n_keys, const int32_t* vblocks,
+                         int64_t n_vblocks, const uint8_t* mask, int32_t block_rows,
+                         float softmax_scale, void* out, void* stream);
+
+/*
+ * Host-side validators (host pointers; no GPU needed). They return FDL_ERR_RANGE with a
+ * message naming the first offending entry.
+ */
+/* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
+ * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
+int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,
+                      int64_t n_kv_rows, int64_t n_rope_rows, int32_t kv_packed);
+/* work items, their row lists and page-table entries lie inside their buffers. */
+int fdl_validate_work(const int32_t* work, int64_t n_work, const int32_t* row_idx,
+                      int64_t n_row_idx, int64_t n_q_rows, const int32_t* page_table,
+                      int64_t n_seq, int64_t max_pages, int32_t page_log2, int64_t n_slots);
+/* verify blocks and their key lists lie inside their buffers. */
+int fdl_validate_vblocks(const int32_t* vblocks, int64_t n_vblocks, const int64_t* key_slots,
+                         int64_t n_keys, int64_t n_q_rows, int64_t n_slots,
+                         int32_t block_rows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FDL_H_ */

@@ -1,0 +1,112 @@
+"""C-ABI library checks that need no GPU: the library loads, exports every entry point
+include/fdl.h declares, and rejects bad arguments on the host before any GPU work."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from fdl import lib
+from fdl.schedule import SeqRows, build_work, contiguous_page_table
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "fdl.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fdl_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.load()
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(lib.SIGNATURES), "ctypes signatures out of sync with fdl.h"
+    assert L.fdl_abi_version() == 1
+
+
+def _expect(status, name, *args):
+    with pytest.raises(lib.FdlError) as ei:
+        lib.call(name, *args)
+    assert ei.value.status == status
+    return str(ei.value)
+
+
+def test_launchers_reject_bad_scalars_without_gpu():
+    # null pointers, wrong head_dim, inconsistent d_model: all caught before any HIP call
+    msg = _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_qkv_rope_cache", None, None, None, None, None, None,
+                  10, None, None, 4, 4096, 64, 64, None, None, None, 10, 0, None)
+    assert "head_dim" in msg
+    _expect(lib.FDL_ERR_SHAPE, "fdl_qkv_rope_cache", None, None, None, None, None, None,
+            10, None, None, 4, 4000, 32, 128, None, None, None, 10, 0, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_qkv_rope_cache", None, None, None, None, None, None,
+            10, None, None, 4, 4096, 32, 128, None, None, None, 10, 0, None)
+    _expect(lib.FDL_ERR_SHAPE, "fdl_qkv_rope_cache", None, None, None, None, None, None,
+            10, None, None, 4, 4096, 32, 128, None, None, None, 7, 1, None)
+    # zero rows is a no-op
+    lib.call("fdl_qkv_rope_cache", None, None, None, None, None, None, 0, None, None, 0,
+             4096, 32, 128, None, None, None, 0, 0, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128,
+            None, 1, 1, 5, None, 1, None, 1, 0.1, None, 0, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_block_attention", None, None, None, 4, 4, 2048, 32, 64,
+            None, 1, 1, 5, None, 1, None, 1, 0.1, None, 0, None, None)
+    lib.call("fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128, None, 1, 1, 5, None,
+             0, None, 1, 0.1, None, 0, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_importance_rank", None, 10, None, 10, None, 1, 16, None, 0, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32,
+            128, None, 0, None, 1, None, 64, 0.1, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 1,
+            1.0, None, None)
+    assert lib.load().fdl_last_error().decode().startswith("fdl_importance_accumulate")
+
+
+def _arr(a, dt):
+    a = np.ascontiguousarray(a, dtype=dt)
+    return a, a.ctypes.data
+
+
+def test_validate_rows():
+    s, sp = _arr([3, 1, 2], np.int64)
+    lib.call("fdl_validate_rows", sp, None, 3, 8, 8, 0)
+    msg = _expect(lib.FDL_ERR_RANGE, "fdl_validate_rows", sp, None, 3, 3, 8, 0)
+    assert "slot 3" in msg
+    d, dp = _arr([3, 1, 3], np.int64)
+    assert "more than one row" in _expect(lib.FDL_ERR_RANGE, "fdl_validate_rows", dp, None, 3, 8, 8, 0)
+    r, rp = _arr([0, 9, 1], np.int64)
+    assert "rope row 9" in _expect(lib.FDL_ERR_RANGE, "fdl_validate_rows", sp, rp, 3, 8, 8, 0)
+    # packed K/V: duplicate slots are fine (nothing is scattered), rope rows still checked
+    lib.call("fdl_validate_rows", dp, None, 3, 3, 8, 1)
+
+
+def test_validate_work():
+    pt = contiguous_page_table(2, 128)
+    work, rows = build_work([SeqRows(0, 100, np.arange(0, 40), 8), SeqRows(1, 128, np.arange(40, 150))])
+    w, wp = _arr(work, np.int32)
+    r, rp = _arr(rows, np.int32)
+    p, pp = _arr(pt, np.int32)
+    lib.call("fdl_validate_work", wp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 256)
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", wp, len(w), rp, len(r), 149, pp, 2, pt.shape[1], 5, 256)
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", wp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 255)
+    bad = w.copy()
+    bad[0, 2] = 129  # k_end past the page table
+    _, bp = _arr(bad, np.int32)
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", bp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 256)
+    bad = w.copy()
+    bad[0, 4] = 65  # too many rows in a tile
+    _, bp = _arr(bad, np.int32)
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", bp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 256)
+    _expect(lib.FDL_ERR_SHAPE, "fdl_validate_work", wp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 3, 256)
+
+
+def test_validate_vblocks():
+    vb, vp = _arr([[0, 3, 0, 8], [3, 5, 8, 16]], np.int32)
+    ks, kp = _arr([1, 2, 3, 9, 10], np.int64)
+    lib.call("fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 8)
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 10, 8)   # slot 10
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 4, 16, 11, 8)   # k1 > n_keys
+    _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 7)   # 8 rows > 7
+    _expect(lib.FDL_ERR_SHAPE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 65)

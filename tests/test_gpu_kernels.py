@@ -1,0 +1,371 @@
+"""Parity of the HIP kernels (through the C ABI) with the numpy oracle on seeded inputs.
+
+Bars: cache-slot writes and top-k / ranking bit-exact; bf16 Q/K/V/attention outputs within
+atol 2e-2 / rtol 1e-2 of the float32 oracle; importance scores within 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import flash_cache_oracle as orc
+from fdl import lib, ops
+from fdl.schedule import SeqRows, contiguous_page_table, make_plan, seqs_from_reference_blocks
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+ATOL, RTOL = 2e-2, 1e-2
+POISON = 1234.0  # exactly representable in bf16
+
+
+def _bf16(shape, gen, std=1.0):
+    return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rope(L, theta=500000.0, hd=128, repeat=1):
+    sin, cos = orc.rope_tables(L, hd, theta)
+    return (torch.from_numpy(np.tile(sin, (repeat, 1))).to(DEV),
+            torch.from_numpy(np.tile(cos, (repeat, 1))).to(DEV))
+
+
+def _close(got, exp, atol=ATOL, rtol=RTOL, what=""):
+    np.testing.assert_allclose(got, exp, atol=atol, rtol=rtol, err_msg=what)
+
+
+# ------------------------------------------------------------------- fused projection
+
+def _qkv_case(seed, n_heads, Q, n_slots, slots, kv_packed=False, theta=500000.0, L=None):
+    gen = torch.Generator().manual_seed(seed)
+    D = n_heads * 128
+    x = _bf16((Q, D), gen)
+    wq, wk, wv = (_bf16((D, D), gen, 0.02) for _ in range(3))
+    L = L or n_slots
+    sin, cos = _rope(L, theta, repeat=max(1, n_slots // L))
+    slot = torch.as_tensor(slots, dtype=torch.int64)
+    q_out = torch.zeros((Q, D), dtype=torch.bfloat16, device=DEV)
+    rows_kv = Q if kv_packed else n_slots
+    kc = torch.full((rows_kv, D), POISON, dtype=torch.bfloat16, device=DEV)
+    vc = torch.full((rows_kv, D), POISON, dtype=torch.bfloat16, device=DEV)
+    xd, wqd, wkd, wvd = (t.to(DEV) for t in (x, wq, wk, wv))
+    ops.qkv_rope_cache(xd, wqd, wkd, wvd, sin, cos, slot.to(DEV), q_out, kc, vc, n_heads,
+                       kv_packed=kv_packed)
+    torch.cuda.synchronize()
+    s_np, c_np = sin.cpu().numpy(), cos.cpu().numpy()
+    if kv_packed:
+        q_ref, k_ref, v_ref = orc.qkv_proj_cache(_np(x), _np(wq), _np(wk), _np(wv), s_np, c_np,
+                                                 slot.numpy(), n_heads, None, None)
+    else:
+        q_ref, k_ref, v_ref = orc.qkv_proj_cache(
+            _np(x), _np(wq), _np(wk), _np(wv), s_np, c_np, slot.numpy(), n_heads,
+            np.full((n_slots, D), POISON, np.float32), np.full((n_slots, D), POISON, np.float32))
+    return q_out, kc, vc, q_ref, k_ref, v_ref, slot.numpy()
+
+
+def test_qkv_rope_cache_cfg1_shape():
+    """40 query rows (32-token masked block + 8 tracked slots), d_model 4096, 32 heads,
+    theta 5e5, cache of 512 slots: Q/K/V within tolerance, untouched slots bit-exact."""
+    rng = np.random.default_rng(1)
+    slots = np.concatenate([np.arange(192, 224), rng.choice(192, 8, replace=False)])
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(1, 32, 40, 512, slots)
+    _close(_np(q), q_ref, what="Q")
+    _close(_np(kc)[s], k_ref[s], what="K rows")
+    _close(_np(vc)[s], v_ref[s], what="V rows")
+    untouched = np.setdiff1d(np.arange(512), s)
+    assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
+
+
+def test_qkv_rope_cache_cfg2_shape():
+    """512 rows over 8 sequences of a 896-slot stride (32 masked + 32 tracked each)."""
+    rng = np.random.default_rng(2)
+    B, L = 8, 896
+    slots = []
+    for b in range(B):
+        f = 256 + 32 * int(rng.integers(0, 16))
+        slots.append(b * L + np.arange(f, f + 32))
+    for b in range(B):
+        f = int(slots[b][0] - b * L)
+        slots.append(b * L + rng.choice(f, 32, replace=False))
+    slots = np.concatenate(slots)
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(2, 32, 512, B * L, slots, L=L)
+    _close(_np(q), q_ref, what="Q")
+    _close(_np(kc)[s], k_ref[s], what="K rows")
+    _close(_np(vc)[s], v_ref[s], what="V rows")
+    untouched = np.setdiff1d(np.arange(B * L), s)
+    assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
+
+
+@pytest.mark.parametrize("Q", [1, 17, 129, 300])
+def test_qkv_rope_cache_ragged_rows_small_model(Q):
+    rng = np.random.default_rng(Q)
+    slots = rng.choice(1024, Q, replace=False)
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(10 + Q, 4, Q, 1024, slots, theta=10000.0)
+    _close(_np(q), q_ref, what="Q")
+    _close(_np(kc)[s], k_ref[s], what="K rows")
+    _close(_np(vc)[s], v_ref[s], what="V rows")
+    untouched = np.setdiff1d(np.arange(1024), s)
+    assert np.all(_np(kc)[untouched] == POISON)
+
+
+def test_qkv_packed_verify_mode():
+    rng = np.random.default_rng(3)
+    slots = rng.integers(0, 256, 64)  # repeated slots are legal when nothing is scattered
+    q, k, v, q_ref, k_ref, v_ref, _ = _qkv_case(3, 4, 64, 256, slots, kv_packed=True)
+    _close(_np(q), q_ref, what="Q")
+    _close(_np(k), k_ref, what="K packed")
+    _close(_np(v), v_ref, what="V packed")
+
+
+# ------------------------------------------------------------------ block attention
+
+def _ref_tables(B, L, k_ends, masked_n, tracked):
+    """Reference-format packed schedule: masked rows of every sequence, then tracked rows
+    (llada/generate.py:146-167). Returns (slots, masked_blocks, tracked_blocks)."""
+    slots, masked, tracked_b = [], [], []
+    acc = 0
+    for b in range(B):
+        f = masked_n[b][0]
+        s = b * L + np.arange(f, f + masked_n[b][1])
+        masked.append(orc.make_blocks(b, k_ends, acc, acc + len(s), 32))
+        slots.append(s)
+        acc += len(s)
+    for b in range(B):
+        s = b * L + np.asarray(tracked[b], dtype=np.int64)
+        if len(s):
+            tracked_b.append(orc.make_blocks(b, k_ends, acc, acc + len(s), 32))
+            slots.append(s)
+            acc += len(s)
+    return (np.concatenate(slots), np.concatenate(masked),
+            np.concatenate(tracked_b) if tracked_b else np.zeros((0, 4), np.int64))
+
+
+def _attn_inputs(seed, Q, n_slots, n_heads):
+    gen = torch.Generator().manual_seed(seed)
+    D = n_heads * 128
+    return _bf16((Q, D), gen), _bf16((n_slots, D), gen), _bf16((n_slots, D), gen)
+
+
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM])
+def test_block_attention_cfg2_shape(imp_mode):
+    """8 sequences, k_end 768 of a 896 stride, 32 masked + 32 tracked rows each, 32 heads;
+    masked and tracked rows share one tile per sequence."""
+    rng = np.random.default_rng(4)
+    B, L, H = 8, 896, 32
+    k_ends = [768] * B
+    masked_n, tracked = [], []
+    for b in range(B):
+        f = 256 + 32 * int(rng.integers(0, 16))
+        masked_n.append((f, 32))
+        tracked.append(rng.choice(f, 32, replace=False))
+    slots, mb, tb = _ref_tables(B, L, k_ends, masked_n, tracked)
+    Q = len(slots)
+    q, kc, vc = _attn_inputs(5, Q, B * L, H)
+    plan = make_plan(seqs_from_reference_blocks(mb, tb, importance=imp_mode != lib.IMP_NONE),
+                     contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    assert plan.n_work == B  # one tile per sequence
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(B * L, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    qd, kd, vd = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    ops.block_attention(qd, kd, vd, plan, out, H, scale, imp_mode, imp if imp_mode else None)
+    if imp_mode:
+        ops.importance_accumulate(imp, plan, 1.0 / (32 * H) if imp_mode == lib.IMP_RAW_LOGIT else 1.0, scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    ref = orc.block_attention(qn, kn, vn, np.concatenate([mb, tb]), L, H, scale)
+    _close(_np(out), ref, what="attention out")
+    if imp_mode == lib.IMP_RAW_LOGIT:
+        S = orc.importance_raw_S(qn, kn, mb, B, L, H, 32)
+        exp = orc.importance_accumulate(np.zeros(B * L, np.float32), S)
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="raw importance")
+    elif imp_mode == lib.IMP_SOFTMAX_COLSUM:
+        exp = orc.importance_softmax_colsum(qn, kn, mb, B, L, H, scale)
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
+
+
+def test_block_attention_paged_stress():
+    """Block-table stress: 6 sequences, k_end in [512, 1536], query lengths in [1, 96] or a
+    full recompute (q = k), 32-slot pages randomly permuted over a global pool."""
+    rng = np.random.default_rng(6)
+    B, H, P = 6, 4, 32
+    k_ends = [int(rng.integers(512, 1537)) for _ in range(B)]
+    k_ends[1] = 1536
+    max_pages = 1536 // P
+    n_pages = sum((k + P - 1) // P for k in k_ends) + 7
+    perm = rng.permutation(n_pages)
+    table = np.zeros((B, max_pages), np.int32)
+    nxt = 0
+    for b in range(B):
+        for p in range((k_ends[b] + P - 1) // P):
+            table[b, p] = perm[nxt]
+            nxt += 1
+    seqs, row = [], 0
+    for b in range(B):
+        qn = k_ends[b] if b in (1, 4) else int(rng.integers(1, 97))
+        rows = np.arange(row, row + qn)
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=rows, n_imp=min(qn, 32)))
+        row += qn
+    Q = row
+    q, kc, vc = _attn_inputs(7, Q, n_pages * P, H)
+    plan = make_plan(seqs, table, 5, device=DEV)
+    plan.validate(Q, n_pages * P)
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, n_pages * P), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(n_pages * P, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, lib.IMP_RAW_LOGIT, imp)
+    ops.importance_accumulate(imp, plan, 1.0, scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    got = _np(out)
+    sc = scores.cpu().numpy()
+    for sq in seqs:
+        blk = np.array([[sq.batch, sq.k_end, sq.rows[0], sq.rows[-1] + 1]])
+        ref = orc.block_attention(qn, kn, vn, blk, 0, H, scale, page_table=table, page_size=P)
+        _close(got[sq.rows], ref[sq.rows], what=f"seq {sq.batch}")
+        keys = orc.key_slots(sq.batch, sq.k_end, 0, table, P)
+        exp = np.zeros(len(keys))
+        for h in range(H):
+            cols = slice(h * 128, (h + 1) * 128)
+            exp += (qn[sq.rows[:sq.n_imp]][:, cols] @ kn[keys][:, cols].T).sum(0)
+        _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"importance seq {sq.batch}")
+
+
+def test_block_attention_leaves_other_rows_untouched():
+    B, L, H = 2, 128, 2
+    seqs = [SeqRows(0, 100, np.array([5, 1, 9])), SeqRows(1, 128, np.array([0, 7]))]
+    q, kc, vc = _attn_inputs(8, 12, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    out = torch.full((12, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, 0.088)
+    torch.cuda.synchronize()
+    got = _np(out)
+    written = [5, 1, 9, 0, 7]
+    assert np.all(got[np.setdiff1d(np.arange(12), written)] == POISON)
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    _close(got[[5, 1, 9]], orc.attend(qn[[5, 1, 9]], kn[:100], vn[:100], H, 0.088))
+    _close(got[[0, 7]], orc.attend(qn[[0, 7]], kn[L:2 * L], vn[L:2 * L], H, 0.088))
+
+
+# ------------------------------------------------------------------------- ranking
+
+def test_importance_rank_bit_exact():
+    rng = np.random.default_rng(9)
+    B, L = 8, 896
+    scores = (rng.integers(-40, 40, B * L).astype(np.float32) * np.float32(0.25))
+    scores[rng.choice(B * L, 50)] = -0.0
+    full_pos = np.arange(B * L, dtype=np.int64).reshape(B, L)
+    for b in range(B):
+        full_pos[b] = full_pos[b][rng.permutation(L)]
+    lens = [int(rng.integers(0, L)) for _ in range(B)]
+    lens[0], lens[1] = 0, 1
+    seg = np.array([[b * L, lens[b]] for b in range(B)], np.int32)
+    k = 32
+    slots_d = torch.from_numpy(full_pos.copy()).to(DEV)
+    topk_d = torch.zeros((B, k), dtype=torch.int64, device=DEV)
+    ops.importance_rank(torch.from_numpy(scores).to(DEV), slots_d, torch.from_numpy(seg).to(DEV),
+                        max(lens), topk_d, k)
+    torch.cuda.synchronize()
+    got = slots_d.cpu().numpy()
+    for b in range(B):
+        seg_slots = full_pos[b, :lens[b]]
+        np.testing.assert_array_equal(got[b, :lens[b]], orc.rank_ascending(scores, seg_slots))
+        np.testing.assert_array_equal(got[b, lens[b]:], full_pos[b, lens[b]:])
+        np.testing.assert_array_equal(topk_d[b].cpu().numpy(), orc.topk(scores, seg_slots, k))
+
+
+def test_importance_rank_max_segment():
+    rng = np.random.default_rng(10)
+    n = 8192
+    scores = rng.standard_normal(n).astype(np.float32)
+    slots = rng.permutation(n).astype(np.int64)
+    slots_d = torch.from_numpy(slots.copy()).to(DEV)
+    topk_d = torch.zeros((1, 64), dtype=torch.int64, device=DEV)
+    ops.importance_rank(torch.from_numpy(scores).to(DEV), slots_d,
+                        torch.tensor([[0, n]], dtype=torch.int32, device=DEV), n, topk_d, 64)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(slots_d.cpu().numpy(), orc.rank_ascending(scores, slots))
+    np.testing.assert_array_equal(topk_d[0].cpu().numpy(), orc.topk(scores, slots, 64))
+
+
+# -------------------------------------------------------------------------- verify
+
+def _verify_case(seed, n_blk, k_cache_len, H, bm=32):
+    """Verify blocks in the reference layout (llada/generate.py:260-292): T fill rows,
+    S draft rows, S mask rows; keys are all cache slots except fill and candidates."""
+    rng = np.random.default_rng(seed)
+    rows = 2 * bm
+    L = k_cache_len
+    key_pos, vblocks, masks, qslots = [], [], [], []
+    acc_k = 0
+    for j in range(n_blk):
+        S = int(rng.integers(4, bm // 2 + 1))
+        T = rows - 2 * S
+        nd = int(rng.integers(T + 64, L - S - 1))
+        order = np.arange(L)
+        fill = order[nd - T:nd]
+        cand = order[nd:nd + S]
+        keys = np.concatenate([order[:nd - T], order[nd + S:]]) + j * L
+        key_pos.append(keys)
+        vblocks.append((acc_k, acc_k + len(keys), j * rows, (j + 1) * rows))
+        acc_k += len(keys)
+        masks.append(orc.verify_mask(T, S, bm))
+        qslots.append(np.concatenate([fill, cand, cand]) + j * L)
+    return (np.concatenate(key_pos).astype(np.int64), np.asarray(vblocks, np.int32),
+            np.concatenate(masks), np.concatenate(qslots).astype(np.int64))
+
+
+def test_verify_attention_cfg4_shape():
+    """16 verify blocks over 1024-slot caches, S in [4, 16] candidates (2S draft/mask rows)
+    plus fill rows, 32 heads; own-draft masking from the reference's mask construction."""
+    H, bm, n_blk, L = 32, 32, 16, 1024
+    key_pos, vblocks, mask, _ = _verify_case(11, n_blk, L, H, bm)
+    rows = 2 * bm
+    gen = torch.Generator().manual_seed(12)
+    D = H * 128
+    q, k1, v1 = (_bf16((n_blk * rows, D), gen) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen) for _ in range(2))
+    out = torch.full((n_blk * rows, D), POISON, dtype=torch.bfloat16, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.verify_attention(q.to(DEV), k1.to(DEV), v1.to(DEV), kc.to(DEV), vc.to(DEV),
+                         torch.from_numpy(key_pos).to(DEV), torch.from_numpy(vblocks).to(DEV),
+                         torch.from_numpy(mask).to(DEV), rows, out, H, scale)
+    torch.cuda.synchronize()
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, rows, H, scale)
+    _close(_np(out), ref, what="verify attention")
+
+
+def test_verify_end_to_end_projection_and_attention():
+    """Packed verify projection followed by verify attention, as the verify pass runs them
+    (flash_cache_triton.py:499-535)."""
+    H, bm, n_blk, L = 4, 8, 3, 256
+    key_pos, vblocks, mask, qslots = _verify_case(13, n_blk, L, H, bm)
+    rows = 2 * bm
+    gen = torch.Generator().manual_seed(14)
+    D = H * 128
+    Q = n_blk * rows
+    x = _bf16((Q, D), gen)
+    wq, wk, wv = (_bf16((D, D), gen, 0.02) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen) for _ in range(2))
+    sin, cos = _rope(L, 500000.0, repeat=n_blk)
+    q, k1, v1 = (torch.empty((Q, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    ops.qkv_rope_cache(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), sin, cos,
+                       torch.from_numpy(qslots).to(DEV), q, k1, v1, H, kv_packed=True)
+    out = torch.empty((Q, D), dtype=torch.bfloat16, device=DEV)
+    ops.verify_attention(q, k1, v1, kc.to(DEV), vc.to(DEV), torch.from_numpy(key_pos).to(DEV),
+                         torch.from_numpy(vblocks).to(DEV), torch.from_numpy(mask).to(DEV), rows,
+                         out, H, orc.softmax_scale(128))
+    torch.cuda.synchronize()
+    q_ref, k_ref, v_ref = orc.qkv_proj_cache(_np(x), _np(wq), _np(wk), _np(wv), sin.cpu().numpy(),
+                                             cos.cpu().numpy(), qslots, H, None, None)
+    # attention from the kernel's own bf16 projections isolates the attention error
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, rows, H, orc.softmax_scale(128))
+    _close(_np(q), q_ref, what="verify Q")
+    _close(_np(k1), k_ref, what="verify K")
+    _close(_np(out), ref, what="verify attention")
