@@ -1,0 +1,418 @@
+"""Decode scheduler of Flash-dLLM (Flash-Cache + Flash-Verify), restated for this build.
+
+`generate_with_Flash_dLLM` keeps the reference's signature and decisions
+(llada/generate.py:61-472):
+  * slot layout: sequence j owns cache rows [j*L, (j+1)*L) with
+    L = ((max prompt + gen + block_m) // 128 + 1) * 128 (:76-79), k_end = seqlen_k (:122);
+  * step 0 recomputes every slot (masked block + all other slots tracked, :125-134);
+  * each step: forward over the packed rows (masked rows of all sequences, then tracked
+    rows, :146-167, :439-467); confidence = max of the float64 softmax of the masked rows'
+    logits; accept the rows with confidence >= threshold, at least one (:335-350);
+  * Flash-Verify (:210-303, :312-333): the not-accepted masked rows, by confidence, become
+    S = min(len - keep, block_m / 2) candidates; a second forward over
+    [T fill rows, S draft rows, S mask rows] (T = 2 block_m - 2S) against all other cache
+    slots under the verify mask; the candidates' draft tokens are accepted as the prefix
+    whose cumulative probability stays >= gamma;
+  * refresh (:364-381): the previously decoded slots are re-ordered by attention
+    importance (ascending) and the tracked set for the next step is the last
+    track_num * block_m decoded entries plus the look-ahead window;
+  * finished sequences are replaced by the next prompt (:405-427).
+
+What differs from the reference, on purpose:
+  * bookkeeping (token ids, full_pos, per-sequence counters) lives in host numpy arrays,
+    so a step synchronises with the GPU three times (pass-1 confidences, verify
+    probabilities, importance ranking) instead of at every `.item()`;
+  * the logits are computed only for the rows the step reads (the masked rows, the verify
+    mask-view rows); the LM head is row-wise, so the values are the same;
+  * the importance ranking runs on the GPU (fdl_importance_rank) with ties broken toward
+    the lower slot; the reference's torch.sort leaves ties unordered;
+  * sorting the confidences uses a stable order (ties keep row order);
+  * a masked block cut short by the end of the slot row is handled (the reference's
+    verify pass fails on it with a shape mismatch, generate.py:215/:235);
+  * without a tokenizer, responses[i] holds the generated token ids.
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .schedule import SeqRows, contiguous_page_table, make_plan
+
+
+def get_rotary_embedding(seq_len: int, dim: int, rope_theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """sin, cos float32 [seq_len, dim] (llada/generate.py:44-50)."""
+    inv_freq = 1.0 / (rope_theta ** (torch.arange(0, dim, 2, device=device, dtype=torch.float32) / dim))
+    seq = torch.arange(seq_len, device=device, dtype=torch.float32)
+    freqs = torch.outer(seq, inv_freq)
+    positions = torch.cat((freqs, freqs), dim=-1)
+    return positions.sin(), positions.cos()
+
+
+def make_blocks(j: int, seqlen_k, start_m: int, end_m: int, block_m: int) -> np.ndarray:
+    """(batch, k_end, q_start, q_end) rows over [start_m, end_m) (llada/generate.py:52-58)."""
+    starts = np.arange(start_m, end_m, block_m, dtype=np.int64)
+    ends = np.minimum(starts + block_m, end_m)
+    return np.stack([np.full_like(starts, j), np.full_like(starts, seqlen_k[j]), starts, ends], axis=1)
+
+
+def verify_mask(T: int, S: int, block_m: int) -> np.ndarray:
+    """The [2 block_m, 2 block_m] verify mask in closed form (llada/generate.py:262-269):
+    fill rows never see the drafts; draft i sees drafts j <= i and masks j > i; mask i sees
+    drafts j < i and masks j >= i; every other entry is True."""
+    n = 2 * block_m
+    m = np.ones((n, n), dtype=bool)
+    m[:T, T:T + S] = False
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    m[T:T + S, T:T + S] = i >= j
+    m[T:T + S, T + S:T + 2 * S] = i < j
+    m[T + S:T + 2 * S, T:T + S] = i > j
+    m[T + S:T + 2 * S, T + S:T + 2 * S] = i <= j
+    return m
+
+
+@dataclass
+class DecodeStats:
+    steps: int = 0
+    forwards: int = 0
+    rows: int = 0
+    verify_accepted: int = 0  # tokens accepted by the verify pass
+    wall_s: float = 0.0
+    per_step_s: list = field(default_factory=list)
+
+
+class _Seq:
+    __slots__ = ("prompt", "nd", "seqlen_k", "masked", "tracked", "predicted_length",
+                 "decoded_eos", "keep_rows", "verify_pos")
+
+
+def _to_dev(a: np.ndarray, device, dtype=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    if torch.device(device).type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
+
+
+@torch.no_grad()
+def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, responses, n_steps, steps=128,
+                             gen_length=128, block_length=128, temperature=0., remasking='low_confidence',
+                             mask_id=126336, threshold=0.9, gamma=0.9, track_num=4, mask_num=4, eos_id=126081,
+                             verify=False, sliding_window=True, is_instruct=True, tokenizer=None,
+                             stop_tokens=None, stats: DecodeStats | None = None, use_gpu_rank: bool = True,
+                             rows_only: bool = True):
+    """Returns (responses, num_tokens, max_num_tokens) like llada/generate.py:472.
+
+    use_gpu_rank: rank the decoded slots with fdl_importance_rank (else numpy, same order).
+    rows_only: run the LM head only on the rows the step reads (else on every row).
+    """
+    dev = model.device
+    cfg = model.config
+    bm = block_length
+    bn = 128
+    B = batch_size
+    L = ((max(prompt_lengths) + gen_length + bm) // bn + 1) * bn
+    d_model, n_layers, n_heads = cfg.d_model, cfg.n_layers, cfg.n_heads
+    stats = stats if stats is not None else DecodeStats()
+    t_start = time.perf_counter()
+
+    x = np.full(B * L, mask_id, dtype=np.int64)
+    x_draft = np.full(B * L, mask_id, dtype=np.int64)
+    full_pos = np.arange(B * L, dtype=np.int64).reshape(B, L)
+    attn_scores = torch.zeros(B * L, dtype=torch.float32, device=dev)
+    num_tokens = 0
+    max_num_tokens = 0
+    active = [-1] * B
+    seqs = [_Seq() for _ in range(B)]
+    start_layer = [-1] * B
+    count = 0
+
+    def load_prompt(j: int, i: int) -> None:
+        pl = int(prompt_lengths[i])
+        s = seqs[j]
+        x[j * L:(j + 1) * L] = mask_id
+        x[j * L:j * L + pl] = np.asarray(prompts[i], dtype=np.int64)[:pl]
+        x[j * L + pl + gen_length:(j + 1) * L] = eos_id
+        x_draft[j * L:(j + 1) * L] = mask_id
+        x_draft[j * L:j * L + pl] = x[j * L:j * L + pl]
+        full_pos[j] = np.arange(j * L, (j + 1) * L)
+        s.prompt = i
+        s.nd = pl
+        s.seqlen_k = (pl + gen_length) // bn * bn + bn
+        s.masked = full_pos[j, s.nd:s.nd + bm].copy()
+        s.tracked = np.concatenate([full_pos[j, :s.nd], full_pos[j, s.nd + bm:s.seqlen_k]])
+        s.predicted_length = s.nd + gen_length + j * L
+        s.decoded_eos = -1
+        s.keep_rows = 0
+        s.verify_pos = np.zeros(0, np.int64)
+        active[j] = i
+        start_layer[j] = -1
+
+    for j in range(B):
+        load_prompt(j, count)
+        count += 1
+
+    sin, cos = get_rotary_embedding(L, d_model // n_heads, cfg.rope_theta, dev)
+    rope = [sin.repeat(B, 1).contiguous(), cos.repeat(B, 1).contiguous()]
+    for blk in model.model.transformer.blocks:
+        blk.k_cache = torch.empty((L * B, d_model), dtype=model.dtype, device=dev)
+        blk.v_cache = torch.empty((L * B, d_model), dtype=model.dtype, device=dev)
+    page_table = contiguous_page_table(B, L)
+    empty_i32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    full_pos_d = torch.empty(B * L, dtype=torch.int64, device=dev)
+
+    while True:
+        t_step = time.perf_counter()
+        # ---- pack the step's query rows: masked rows, then tracked rows (:439-467)
+        masked_blocks, tracked_blocks, seq_rows = [], [], []
+        acc = 0
+        rows_of = {}
+        for j in range(B):
+            if active[j] != -1 and len(seqs[j].masked):
+                n = len(seqs[j].masked)
+                masked_blocks.append(make_blocks(j, [s.seqlen_k for s in seqs], acc, acc + n, bm))
+                rows_of[j] = [np.arange(acc, acc + n)]
+                acc += n
+        n_masked_rows = acc
+        for j in range(B):
+            if active[j] != -1 and len(seqs[j].tracked):
+                n = len(seqs[j].tracked)
+                tracked_blocks.append(make_blocks(j, [s.seqlen_k for s in seqs], acc, acc + n, bm))
+                rows_of.setdefault(j, [np.zeros(0, np.int64)]).append(np.arange(acc, acc + n))
+                acc += n
+        order_j = [j for j in range(B) if active[j] != -1 and (len(seqs[j].masked) or len(seqs[j].tracked))]
+        qpos = np.concatenate([seqs[j].masked for j in range(B) if active[j] != -1 and len(seqs[j].masked)] +
+                              [seqs[j].tracked for j in range(B) if active[j] != -1 and len(seqs[j].tracked)])
+        for j in order_j:
+            r = rows_of[j]
+            rows = np.concatenate(r)
+            seq_rows.append(SeqRows(batch=j, k_end=seqs[j].seqlen_k, rows=rows,
+                                    n_imp=len(r[0]) if len(seqs[j].masked) else 0))
+        plan = make_plan(seq_rows, page_table, device=dev)
+        mb = np.concatenate(masked_blocks) if masked_blocks else np.zeros((0, 4), np.int64)
+        tb = np.concatenate(tracked_blocks) if tracked_blocks else np.zeros((0, 4), np.int64)
+        mb_t, tb_t = torch.from_numpy(mb), torch.from_numpy(tb)
+        qpos_d = _to_dev(qpos, dev)
+        x_query = _to_dev(x[qpos], dev)[None]
+        positions = [qpos_d, empty_i32, rope, plan, attn_scores, []]
+        lengths = [start_layer, None, mb_t, tb_t, torch.cat([mb_t, tb_t]), active, len(mb), L, bm, bn, None,
+                   False]
+        logit_rows = torch.arange(n_masked_rows, device=dev) if rows_only else None
+        logits = model(x_query, use_cache=True, lengths=lengths, positions=positions,
+                       logit_rows=logit_rows).logits.squeeze(0)[:n_masked_rows]
+        stats.forwards += 1
+        stats.rows += len(qpos)
+        p = F.softmax(logits.to(torch.float64), dim=-1)
+        x0_p_all, x0_all = torch.max(p, dim=-1)
+        x0_p_all = x0_p_all.cpu().numpy()
+        x0_all = x0_all.cpu().numpy()
+        del p, logits
+
+        keep_num = [0] * B
+        acc_masked = 0
+        if verify:
+            x_verify, key_pos, masks, vblocks, vq_pos = [], [], [], [], []
+            acc_q = acc_k = 0
+            verify_meta = {}
+            for j in range(B):
+                if active[j] == -1:
+                    continue
+                s = seqs[j]
+                nm = len(s.masked)
+                # The reference reads block_m rows here (generate.py:215); a masked block
+                # that reached the end of the slot row is shorter, and the reference then
+                # fails on a shape mismatch (:235). Reading the block's own rows is the
+                # same whenever the reference is defined.
+                rows = slice(acc_masked, acc_masked + min(nm, bm))
+                acc_masked += nm
+                s.masked = s.masked[:bm]
+                conf = x0_p_all[rows].copy()
+                toks = x0_all[rows]
+                if s.decoded_eos != -1:
+                    lmask = s.masked >= s.predicted_length
+                    conf[lmask] = 0
+                    length_num = len(s.masked) - int(lmask.sum())
+                else:
+                    length_num = len(s.masked)
+                order = np.argsort(-conf, kind="stable")
+                keep = max(int((conf >= threshold).sum()), 1)
+                x_draft[s.masked] = toks
+                full_pos[j, s.nd:s.nd + len(s.masked)] = s.masked[order]
+                new_pos = full_pos[j, s.nd:s.nd + keep].copy()
+                new_tok = toks[order][:keep]
+                x[new_pos] = new_tok
+                s.nd += keep
+                if s.decoded_eos == -1:
+                    eos_pos = new_pos[new_tok == eos_id]
+                    if len(eos_pos):
+                        s.decoded_eos = int(eos_pos.max())
+                        s.predicted_length = s.decoded_eos + 1
+                S = min(max(length_num - keep, 0), bm // 2)
+                T = 2 * bm - 2 * S
+                if s.nd < T:
+                    raise NotImplementedError(
+                        f"verify needs at least {T} decoded slots before the block (have {s.nd}); "
+                        "use prompts of at least 2 * block_length tokens")
+                s.keep_rows = T
+                cand = full_pos[j, s.nd:s.nd + S].copy()
+                fill = full_pos[j, s.nd - T:s.nd].copy()
+                x_verify.append(np.concatenate([x[fill], x_draft[cand], x[cand]]))
+                s.verify_pos = np.concatenate([fill, cand, cand])
+                keys = np.concatenate([full_pos[j, :s.nd - T], full_pos[j, s.nd + S:s.seqlen_k]])
+                key_pos.append(keys)
+                m = verify_mask(T, S, bm)
+                masks.append(m)
+                vblocks.append((acc_k, acc_k + len(keys), acc_q, acc_q + len(s.verify_pos)))
+                verify_meta[j] = (acc_q, T, S)
+                acc_q += len(s.verify_pos)
+                acc_k += len(keys)
+            vq = np.concatenate([seqs[j].verify_pos for j in range(B) if active[j] != -1])
+            vblocks_d = _to_dev(np.asarray(vblocks, np.int32), dev)
+            key_pos_d = _to_dev(np.concatenate(key_pos).astype(np.int64), dev)
+            mask_d = _to_dev(np.concatenate(masks), dev)
+            vq_d = _to_dev(vq, dev)
+            xq = _to_dev(np.concatenate(x_verify), dev)[None]
+            # only the mask-view rows [T+S, T+2S) of each block are read (:318)
+            lr = np.concatenate([np.arange(a + T + S, a + T + 2 * S) for (a, T, S) in verify_meta.values()])
+            positions = [vq_d, key_pos_d, rope, None, attn_scores, mask_d]
+            lengths = [start_layer, vblocks_d, None, tb_t, None, active, len(mb), L, bm, bn, None, True]
+            if len(lr):
+                vlog = model(xq, use_cache=True, lengths=lengths, positions=positions,
+                             logit_rows=_to_dev(lr, dev) if rows_only else None).logits.squeeze(0)
+                if not rows_only:
+                    vlog = vlog[_to_dev(lr, dev)]
+                stats.forwards += 1
+                stats.rows += len(vq)
+                draft_rows = np.concatenate([np.arange(a + T, a + T + S) for (a, T, S) in verify_meta.values()])
+                draft_tok = _to_dev(np.concatenate(x_verify)[draft_rows], dev)
+                pv = F.softmax(vlog.to(torch.float64), dim=-1).gather(1, draft_tok[:, None]).view(-1)
+                pv = pv.cpu().numpy()
+                del vlog
+            else:
+                pv = np.zeros(0)
+            off = 0
+            for j, (a, T, S) in verify_meta.items():
+                s = seqs[j]
+                if S == 0:
+                    keep_num[j] = 0
+                    continue
+                probs = pv[off:off + S].copy()
+                off += S
+                if s.decoded_eos != -1:
+                    probs[s.verify_pos[T:T + S] >= s.predicted_length] = 0
+                cp = np.cumprod(probs)
+                keep = int((cp >= gamma).sum())
+                keep_num[j] = keep
+                stats.verify_accepted += keep
+                if keep > 0:
+                    new_pos = full_pos[j, s.nd:s.nd + keep].copy()
+                    new_tok = x_draft[s.verify_pos[T:T + keep]]
+                    x[new_pos] = new_tok
+                    s.nd += keep
+                    if s.decoded_eos == -1:
+                        eos_pos = new_pos[new_tok == eos_id]
+                        if len(eos_pos):
+                            s.decoded_eos = int(eos_pos.max())
+                            s.predicted_length = s.decoded_eos + 1
+        else:
+            for j in range(B):
+                if active[j] == -1:
+                    continue
+                s = seqs[j]
+                nm = len(s.masked)
+                rows = slice(acc_masked, acc_masked + nm)
+                acc_masked += nm
+                conf = x0_p_all[rows].copy()
+                toks = x0_all[rows]
+                if s.decoded_eos != -1:
+                    conf[s.masked >= s.predicted_length] = 0
+                order = np.argsort(-conf, kind="stable")
+                keep = max(int((conf[order] >= threshold).sum()), 1)
+                full_pos[j, s.nd:s.nd + nm] = s.masked[order]
+                new_pos = full_pos[j, s.nd:s.nd + keep].copy()
+                new_tok = toks[order][:keep]
+                keep_num[j] = keep
+                x[new_pos] = new_tok
+                s.nd += keep
+                if s.decoded_eos == -1:
+                    eos_pos = new_pos[new_tok == eos_id]
+                    if len(eos_pos):
+                        s.decoded_eos = int(eos_pos.max())
+                        s.predicted_length = s.decoded_eos + 1
+
+        # ---- importance refresh (:364-381) and sequence completion (:385-433)
+        cont = []
+        for j in range(B):
+            if active[j] == -1:
+                continue
+            s = seqs[j]
+            n_steps[active[j]] += 1
+            if (full_pos[j, s.nd:] < s.predicted_length).any():
+                cont.append(j)
+            else:
+                i = active[j]
+                pl = int(prompt_lengths[i])
+                gen_ids = x[j * L + pl: j * L + s.nd].copy()
+                if tokenizer is not None:
+                    text = tokenizer.decode(gen_ids, skip_special_tokens=False)
+                    for stop_seq in (stop_tokens or []):
+                        if stop_seq in text:
+                            text = text.split(stop_seq)[0]
+                    ids = tokenizer(text)["input_ids"]
+                    responses[i] = tokenizer.decode(ids, skip_special_tokens=True)
+                else:
+                    responses[i] = gen_ids.tolist()
+                num_tokens += s.nd - pl
+                max_num_tokens += gen_length
+                if count < len(prompts):
+                    load_prompt(j, count)
+                    count += 1
+                else:
+                    active[j] = -1
+                    s.masked = np.zeros(0, np.int64)
+                    s.tracked = np.zeros(0, np.int64)
+                    s.verify_pos = np.zeros(0, np.int64)
+        if cont:
+            segs = np.array([[j * L, seqs[j].nd - keep_num[j]] for j in cont], dtype=np.int32)
+            if use_gpu_rank:
+                full_pos_d.copy_(torch.from_numpy(full_pos.reshape(-1)), non_blocking=False)
+                ops.importance_rank(attn_scores, full_pos_d, _to_dev(segs, dev), int(segs[:, 1].max()))
+                fp = full_pos_d.cpu().numpy().reshape(B, L)
+                for j in cont:
+                    n = seqs[j].nd - keep_num[j]
+                    full_pos[j, :n] = fp[j, :n]
+            else:
+                sc = attn_scores.cpu().numpy()
+                for j in cont:
+                    n = seqs[j].nd - keep_num[j]
+                    seg = full_pos[j, :n]
+                    v = sc[seg]
+                    v = np.where(v == 0, np.float32(0), v)
+                    full_pos[j, :n] = seg[np.lexsort((-seg, v))]
+            for j in cont:
+                s = seqs[j]
+                s.masked = full_pos[j, s.nd:s.nd + bm].copy()
+                if track_num < 0:
+                    s.tracked = np.concatenate([full_pos[j, :s.nd], full_pos[j, s.nd + bm:s.seqlen_k]])
+                else:
+                    t0 = max(0, s.nd - track_num * bm)
+                    t1 = min(s.seqlen_k, s.nd + bm * mask_num)
+                    s.tracked = np.concatenate([full_pos[j, t0:s.nd], full_pos[j, s.nd + bm:t1]])
+                start_layer[j] = n_layers
+        stats.steps += 1
+        stats.per_step_s.append(time.perf_counter() - t_step)
+        if all(a == -1 for a in active):
+            break
+        attn_scores.zero_()
+
+    if torch.device(dev).type == "cuda":
+        torch.cuda.synchronize(dev)
+    stats.wall_s = time.perf_counter() - t_start
+    return responses, num_tokens, max_num_tokens

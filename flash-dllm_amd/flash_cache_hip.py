@@ -1,0 +1,146 @@
+"""Drop-in replacement of `flash_cache_triton.flash_fused_elastic_cache` for MI355X.
+
+    from flash_cache_hip import flash_fused_elastic_cache
+
+has the signature and the side effects of the reference driver
+(llada/flash_cache_triton.py:462-638): it runs one transformer block for the packed query
+rows of a denoising step and returns the block output [1, Q, d_model]. The attention
+half runs on the hand-written gfx950 kernels behind the C ABI (include/fdl.h):
+
+  non-verify pass (flash_cache_triton.py:536-615)
+    fdl_qkv_rope_cache       Q packed by row; K/V written to self.k_cache/self.v_cache at
+                             query_pos_flat (replaces _flash_qkv_proj_cache_fwd)
+    fdl_block_attention      masked and tracked rows of a sequence in one tile (replaces
+                             _flash_masked_attention_fwd + _flash_tracked_attention_fwd)
+    fdl_importance_accumulate  attn_scores += mean over (block_m rows, heads) of the raw
+                             logits of the masked rows, for block_idx > 1 (replaces the
+                             S buffer and `attn_scores += S.mean((0, 1))`)
+  verify pass (flash_cache_triton.py:499-535)
+    fdl_qkv_rope_cache       kv_packed: Q/K/V of the verify rows, cache untouched
+    fdl_verify_attention     cache keys through key_pos_flat + in-block keys under attn_mask
+
+The MLP half (attn_out, residual, ff_norm, SiLU-gated MLP, residual; :618-636) stays in
+torch, as in the reference.
+
+positions = [query_pos_flat, key_pos_flat, [sin, cos], info, attn_scores, attn_mask]
+lengths   = [start_layer, query_verify_blocks, query_masked_blocks, query_tracked_blocks,
+             query_blocks, active_batch, num_active, max_length, block_m, block_n,
+             elastic_cache, verify]
+`info` (unused by the reference kernels) may carry a precomputed fdl.schedule.AttnPlan;
+otherwise the plan is derived from the masked/tracked block tables once per forward
+(the same table objects are passed to every layer) and reused by all layers.
+"""
+from __future__ import annotations
+
+import math
+import weakref
+
+import numpy as np
+import torch
+
+from fdl import lib as _lib
+from fdl import ops
+from fdl.schedule import AttnPlan, contiguous_page_table, make_plan, seqs_from_reference_blocks
+
+_plan_cache: dict = {}
+_workspace: dict = {}
+
+
+def _as_np_table(t) -> np.ndarray:
+    if t is None or (isinstance(t, (list, tuple)) and len(t) == 0):
+        return np.zeros((0, 4), dtype=np.int64)
+    return t.detach().to("cpu").numpy().astype(np.int64).reshape(-1, 4)
+
+
+def _plan_from_tables(masked, tracked, n_seq: int, max_length: int, device) -> AttnPlan:
+    """AttnPlan for the reference's block tables, cached on the identity of the tables."""
+    key = (id(masked), id(tracked), n_seq, max_length, str(device))
+    hit = _plan_cache.get("entry")
+    if hit is not None and hit[0] == key and hit[1]() is masked and hit[2]() is tracked:
+        return hit[3]
+    seqs = seqs_from_reference_blocks(_as_np_table(masked), _as_np_table(tracked), importance=True)
+    plan = make_plan(seqs, contiguous_page_table(n_seq, max_length), device=device)
+    ref = lambda t: weakref.ref(t) if isinstance(t, torch.Tensor) else (lambda: t)  # noqa: E731
+    _plan_cache["entry"] = (key, ref(masked), ref(tracked), plan)
+    return plan
+
+
+def _imp_workspace(n_heads: int, n_slots: int, device) -> torch.Tensor:
+    key = (n_heads, n_slots, str(device))
+    ws = _workspace.get(key)
+    if ws is None:
+        ws = torch.empty((n_heads, n_slots), dtype=torch.float32, device=device)
+        _workspace.clear()
+        _workspace[key] = ws
+    return ws
+
+
+def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
+    """attn_out + residual + SiLU-gated MLP + residual (flash_cache_triton.py:618-638)."""
+    att = self.attn_out(att)
+    x = x + self.dropout(att)
+    og_x = x
+    if self._activation_checkpoint_fn is not None:
+        x = self._activation_checkpoint_fn(self.ff_norm, x)
+    else:
+        x = self.ff_norm(x)
+    x, x_up = self.ff_proj(x), self.up_proj(x)
+    if self._activation_checkpoint_fn is not None:
+        x = self._activation_checkpoint_fn(self.act, x)
+    else:
+        x = self.act(x)
+    x = x * x_up
+    x = self.ff_out(x)
+    x = self.dropout(x)
+    x = og_x + x
+    return x.unsqueeze(0)
+
+
+def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengths,
+                              softmax_scale: float = None):
+    """One transformer block over the packed query rows (see the module docstring)."""
+    query_pos_flat, key_pos_flat, rotary_emb_pos, info, attn_scores, attn_mask = positions
+    (start_layer, query_verify_blocks, query_masked_blocks, query_tracked_blocks, query_blocks,
+     active_batch, num_active, max_length, block_m, block_n, elastic_cache, verify) = lengths
+
+    d_model = self.config.d_model
+    n_heads = self.config.n_heads
+    head_dim = d_model // n_heads
+    batch_size = len(active_batch)
+    softmax_scale = softmax_scale or (1.0 / math.sqrt(head_dim))
+
+    x_normed = self.attn_norm(x)
+    att = torch.empty_like(x)
+    q = torch.empty_like(x)
+    sin, cos = rotary_emb_pos[0], rotary_emb_pos[1]
+
+    if verify:
+        k = torch.empty_like(x)
+        v = torch.empty_like(x)
+        if query_verify_blocks is not None and query_verify_blocks.shape[0] > 0:
+            ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,
+                               self.v_proj.weight, sin, cos, query_pos_flat, q, k, v, n_heads,
+                               kv_packed=True)
+            keys = key_pos_flat
+            if not isinstance(keys, torch.Tensor) or keys.dtype != torch.int64:
+                keys = torch.as_tensor(keys, dtype=torch.int64, device=x.device)
+            ops.verify_attention(q, k, v, self.k_cache, self.v_cache, keys,
+                                 query_verify_blocks, attn_mask, 2 * block_m, att, n_heads,
+                                 softmax_scale)
+    else:
+        n_rows = x.shape[0]
+        if n_rows > 0:
+            ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,
+                               self.v_proj.weight, sin, cos, query_pos_flat, q, self.k_cache,
+                               self.v_cache, n_heads)
+            plan = info if isinstance(info, AttnPlan) else _plan_from_tables(
+                query_masked_blocks, query_tracked_blocks, batch_size, max_length, x.device)
+            importance = block_idx > 1 and plan.has_importance
+            ws = _imp_workspace(n_heads, self.k_cache.shape[0], x.device) if importance else None
+            ops.block_attention(q, self.k_cache, self.v_cache, plan, att, n_heads, softmax_scale,
+                                _lib.IMP_RAW_LOGIT if importance else _lib.IMP_NONE, ws)
+            if importance:
+                # S.mean((0, 1)) divides by block_m * n_heads (flash_cache_triton.py:538, :615)
+                ops.importance_accumulate(ws, plan, 1.0 / (block_m * n_heads), attn_scores)
+
+    return block_mlp_tail(self, x, att)
