@@ -204,6 +204,61 @@ def run_cpu_baseline(budget_s: float = 15.0, seed: int = 2) -> dict:
                       f"host os.cpu_count()={os.cpu_count()}"}
 
 
+E2E = dict(batch=8, prompt=256, gen=512, block=32, track_num=1, mask_num=1, threshold=0.9,
+           gamma=0.9, verify=True)
+
+
+def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0) -> dict:
+    """Random-init LLaDA-8B (32 layers, d_model 4096, SiLU-gated MLP 12288, vocab 126464,
+    bf16) under the Flash-Cache + Flash-Verify decode loop: batch 8, 256-token random
+    prompts, 512 generated tokens, block 32, 32 tracked tokens, verify eps = gamma = 0.9.
+    tokens/s = decoded tokens / wall seconds of the decode loop (GPU-synchronised)."""
+    import torch
+    from flash_cache_hip import flash_fused_elastic_cache
+    from fdl.generate import DecodeStats, generate_with_Flash_dLLM
+    from fdl.model import LLaDAConfig, build_model
+    from fdl.torch_path import flash_fused_elastic_cache_torch
+
+    dev = torch.device("cuda:0")
+    cfg = LLaDAConfig.llada_8b()
+    model = build_model(cfg, flash_fused_elastic_cache, dev, torch.bfloat16, seed=seed)
+    rng = np.random.default_rng(seed)
+    n = E2E["batch"]
+    prompts = []
+    for _ in range(n):
+        p = rng.integers(0, cfg.vocab_size, E2E["prompt"])
+        p[(p == cfg.mask_token_id) | (p == cfg.eos_token_id)] = 0
+        prompts.append(torch.from_numpy(p))
+    lengths = [E2E["prompt"]] * n
+    kw = dict(gen_length=E2E["gen"], block_length=E2E["block"], mask_id=cfg.mask_token_id,
+              threshold=E2E["threshold"], gamma=E2E["gamma"], track_num=E2E["track_num"],
+              mask_num=E2E["mask_num"], eos_id=cfg.eos_token_id, verify=E2E["verify"])
+
+    def decode(steps):
+        st = DecodeStats()
+        generate_with_Flash_dLLM(model, prompts, lengths, n, [None] * n, [0] * n, stats=st,
+                                 max_steps=steps, **kw)
+        return st
+
+    decode(2)  # warm-up: library GEMM selection, allocator
+    st = decode(max_steps)
+    out = {"tokens_per_s": st.decoded / st.wall_s, "decoded_tokens": st.decoded,
+           "steps": st.steps, "forwards": st.forwards, "wall_s": round(st.wall_s, 3),
+           "ms_per_step": round(1e3 * st.wall_s / max(st.steps, 1), 3),
+           "verify_accepted": st.verify_accepted}
+    if torch_steps > 0:
+        model.set_attention(flash_fused_elastic_cache_torch)
+        stt = decode(torch_steps)
+        model.set_attention(flash_fused_elastic_cache)
+        out["torch_gpu"] = {"tokens_per_s": stt.decoded / stt.wall_s, "steps": stt.steps,
+                            "ms_per_step": round(1e3 * stt.wall_s / max(stt.steps, 1), 3),
+                            "sample": f"first {stt.steps} steps (incl. the full-recompute step 0) "
+                                      "of the same decode with the unfused PyTorch driver"}
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description="Flash-Cache hot-path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +266,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-e2e", action="store_true", help="skip the LLaDA-8B decode leg")
+    ap.add_argument("--e2e-steps", type=int, default=None,
+                    help="bound the HIP decode to this many steps (default: run to completion)")
+    ap.add_argument("--e2e-torch-steps", type=int, default=24,
+                    help="steps of the unfused PyTorch driver decode (0: skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -258,6 +318,8 @@ def main() -> int:
                      "traffic": None, "kernel": "qkv_rope_cache"},
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
+    if not args.no_e2e:
+        out["e2e_llada8b"] = run_e2e(args.e2e_steps, args.e2e_torch_steps)
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(args.cpu_budget)
     print(json.dumps(out), flush=True)

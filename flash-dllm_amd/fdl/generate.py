@@ -83,6 +83,7 @@ class DecodeStats:
     forwards: int = 0
     rows: int = 0
     verify_accepted: int = 0  # tokens accepted by the verify pass
+    decoded: int = 0          # tokens decoded (both passes), finished or not
     wall_s: float = 0.0
     per_step_s: list = field(default_factory=list)
 
@@ -107,11 +108,13 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                              mask_id=126336, threshold=0.9, gamma=0.9, track_num=4, mask_num=4, eos_id=126081,
                              verify=False, sliding_window=True, is_instruct=True, tokenizer=None,
                              stop_tokens=None, stats: DecodeStats | None = None, use_gpu_rank: bool = True,
-                             rows_only: bool = True):
+                             rows_only: bool = True, max_steps: int | None = None):
     """Returns (responses, num_tokens, max_num_tokens) like llada/generate.py:472.
 
     use_gpu_rank: rank the decoded slots with fdl_importance_rank (else numpy, same order).
     rows_only: run the LM head only on the rows the step reads (else on every row).
+    max_steps: stop after this many denoising steps (benchmarking a bounded sample;
+        stats.decoded then counts the tokens decoded so far).
     """
     dev = model.device
     cfg = model.config
@@ -249,6 +252,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 new_tok = toks[order][:keep]
                 x[new_pos] = new_tok
                 s.nd += keep
+                stats.decoded += keep
                 if s.decoded_eos == -1:
                     eos_pos = new_pos[new_tok == eos_id]
                     if len(eos_pos):
@@ -311,6 +315,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 keep = int((cp >= gamma).sum())
                 keep_num[j] = keep
                 stats.verify_accepted += keep
+                stats.decoded += keep
                 if keep > 0:
                     new_pos = full_pos[j, s.nd:s.nd + keep].copy()
                     new_tok = x_draft[s.verify_pos[T:T + keep]]
@@ -341,6 +346,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 keep_num[j] = keep
                 x[new_pos] = new_tok
                 s.nd += keep
+                stats.decoded += keep
                 if s.decoded_eos == -1:
                     eos_pos = new_pos[new_tok == eos_id]
                     if len(eos_pos):
@@ -409,6 +415,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         stats.steps += 1
         stats.per_step_s.append(time.perf_counter() - t_step)
         if all(a == -1 for a in active):
+            break
+        if max_steps is not None and stats.steps >= max_steps:
             break
         attn_scores.zero_()
 

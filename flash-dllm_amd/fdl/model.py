@@ -178,4 +178,5 @@ def build_model(cfg: LLaDAConfig, attention_fn: Callable, device, dtype=torch.bf
     with torch.device(device):
         model = LLaDAModelLM(cfg, attention_fn, device=device, dtype=dtype)
     model.eval()
+    model.requires_grad_(False)  # inference only
     return random_init_(model, seed)

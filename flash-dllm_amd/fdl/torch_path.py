@@ -74,16 +74,16 @@ def flash_fused_elastic_cache_torch(self, x: torch.Tensor, block_idx, positions,
         rows = 2 * block_m
         for vi, (k0, k1, q0, q1) in enumerate(blocks):
             cache = key_pos_flat[k0:k1]
-            keys = torch.cat([self.k_cache[cache], k[q0:q1]], dim=0)
-            vals = torch.cat([self.v_cache[cache], v[q0:q1]], dim=0)
+            keys = torch.cat([self.k_cache[cache].to(k.dtype), k[q0:q1]], dim=0)
+            vals = torch.cat([self.v_cache[cache].to(v.dtype), v[q0:q1]], dim=0)
             nr = q1 - q0
             allow = torch.ones((nr, k1 - k0 + nr), dtype=torch.bool, device=x.device)
             allow[:, k1 - k0:] = attn_mask[vi * rows: vi * rows + nr, :nr].bool()
             att[q0:q1], _ = _attend(q[q0:q1], keys, vals, n_heads, softmax_scale, allow)
     else:
         if x.shape[0] > 0:
-            self.k_cache.index_copy_(0, pos, k)
-            self.v_cache.index_copy_(0, pos, v)
+            self.k_cache.index_copy_(0, pos, k.to(self.k_cache.dtype))
+            self.v_cache.index_copy_(0, pos, v.to(self.v_cache.dtype))
         importance = block_idx > 1
         S_mean = None
         if importance:
