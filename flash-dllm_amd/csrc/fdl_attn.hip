@@ -8,15 +8,21 @@
 // and _flash_verify_attention_fwd (flash_cache_triton.py:341-428): cache keys gathered
 // through a slot list followed by the block's own rows as keys under a boolean mask.
 //
-// One workgroup = one tile (up to 64 query rows of one sequence) x one head; 4
-// wavefronts, 16 query rows each. Keys stream through LDS 64 at a time: K row-major with
-// XOR-swizzled 16-byte chunks, V transposed (V^T, padded rows). Each wavefront computes
-// S^T = K Q^T with 16x16x32 MFMAs, so lane l holds the logits of query row l % 16 for
-// keys 4*(l/16) + i of every 16-key block: the online-softmax row max and row sum need
-// only two cross-lane steps (xor 16, xor 32), and the bf16 probabilities are already the
-// B operand of O^T = V^T P^T. Importance needs column sums over query rows instead, so
-// it uses S = Q K^T (the same registers with the operands swapped): the sum over rows is
-// then 4 in-lane adds plus the same two cross-lane steps.
+// Workgroup = one tile (up to 64*RB query rows of one sequence) x one head, split into NG
+// key groups of 4 wavefronts. Group g streams its share of the tile's 64-key blocks
+// through its own LDS buffers (K row-major with XOR-swizzled 16-byte chunks, V transposed
+// with padded rows); the next block's global loads are issued into registers before the
+// current block is computed, so HBM latency overlaps the MFMA work. With NG = 2 a tile
+// has two key streams in flight; the groups' partial (max, sum, O) are merged through
+// LDS at the end (exact: rescaled by exp of the max difference).
+//
+// Each wavefront owns RB blocks of 16 query rows and computes S^T = K Q^T with 16x16x32
+// MFMAs, so lane l holds the logits of row l % 16 for keys 4*(l/16) + i of each 16-key
+// block: the online-softmax max and sum need two cross-lane steps (xor 16, xor 32), and
+// the bf16 probabilities are already the B operand of O^T = V^T P^T. The K and V^T
+// fragments read from LDS are shared by the RB row blocks. Importance needs column sums
+// over rows instead, so it uses S = Q K^T (the same registers, operands swapped): 4
+// in-lane adds plus the same two cross-lane steps.
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -24,10 +30,9 @@ namespace fdl {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kTileN = 64;     // keys per LDS tile
-constexpr int kMaxRows = 64;   // query rows per workgroup (4 wavefronts x 16)
-constexpr int kThreads = 256;
-constexpr int kVtStride = 68;  // bf16 per V^T row in LDS (136 B: conflict-free column reads)
+constexpr int kTileN = 64;        // keys per LDS block
+constexpr int kGroupThreads = 256;
+constexpr int kVtStride = 68;     // bf16 per V^T row in LDS (136 B: conflict-free column reads)
 
 struct AttnArgs {
   const uint16_t* q;
@@ -52,159 +57,201 @@ struct AttnArgs {
   int page_log2;
   int d_model;
   int block_rows;
+  int tile_rows;
   int imp_mode;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
-struct TileState {
-  float m;      // running max of this lane's row (log2 domain)
-  float l;      // this lane's partial row sum
-  f32x4 o[8];   // O^T blocks: lane holds O[row l%16][16*db + 4*(l/16) + i]
+struct GroupLds {
+  u32x4 K[kTileN * 16];                   // 16 KB
+  uint32_t Vt[kHeadDim * kVtStride / 2];  // 17 KB
 };
 
-__device__ __forceinline__ float wave_max16x4(float v) {
+struct TileRegs {
+  u32x4 k[4];
+  u32x4 v[2][2];
+};
+
+template <int RB>
+struct RowState {
+  float m[RB];      // running max of the lane's rows (log2 domain)
+  float l[RB];      // partial row sums
+  f32x4 o[RB][8];   // O^T blocks: lane holds O[row][16*db + 4*(l/16) + i]
+};
+
+__device__ __forceinline__ float xmax(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  return fmaxf(v, __shfl_xor(v, 32));
 }
-__device__ __forceinline__ float wave_sum16x4(float v) {
+__device__ __forceinline__ float xsum(float v) {
   v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return v + __shfl_xor(v, 32);
 }
 
-// Loads K (and V^T unless kOnlyK) of keys n0 .. n0+63 into LDS. slot_of(n) gives the
-// cache row of key n (valid for n < n_end); keys at or past n_end load as zeros.
+// Global loads of keys n0 .. n0+63 (K, and V unless kOnlyK) into registers; tg is the
+// thread's index in its key group. Keys at or past n_end load as zeros.
 template <bool kOnlyK, typename SlotOf>
-__device__ __forceinline__ void load_kv_tile(u32x4* Ks, uint32_t* Vt, const uint16_t* kbase,
-                                             const uint16_t* vbase, int64_t D, int col0, int n0,
-                                             int n_end, SlotOf slot_of) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void tile_issue(TileRegs& r, int tg, const uint16_t* kbase,
+                                           const uint16_t* vbase, int64_t D, int col0, int n0,
+                                           int n_end, SlotOf slot_of) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int id = tid + kThreads * i;
-    const int kk = id >> 4, c = id & 15;
-    const int n = n0 + kk;
-    u32x4 val = {0, 0, 0, 0};
-    if (n < n_end) val = ld16(kbase + slot_of(n) * D + col0 + 8 * c);
-    Ks[kk * 16 + (c ^ (kk & 15))] = val;
+    const int id = tg + kGroupThreads * i;
+    const int n = n0 + (id >> 4);
+    r.k[i] = u32x4{0, 0, 0, 0};
+    if (n < n_end) r.k[i] = ld16(kbase + slot_of(n) * D + col0 + 8 * (id & 15));
   }
   if constexpr (!kOnlyK) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int id = tid + kThreads * i;
+      const int id = tg + kGroupThreads * i;
+      const int na = n0 + 2 * (id >> 4);
+      const int c = id & 15;
+      r.v[i][0] = u32x4{0, 0, 0, 0};
+      r.v[i][1] = u32x4{0, 0, 0, 0};
+      if (na < n_end) r.v[i][0] = ld16(vbase + slot_of(na) * D + col0 + 8 * c);
+      if (na + 1 < n_end) r.v[i][1] = ld16(vbase + slot_of(na + 1) * D + col0 + 8 * c);
+    }
+  }
+}
+
+// Registers -> LDS: K chunk c of key kk at chunk c ^ (kk & 15); V transposed, two keys per
+// 32-bit word (V^T[dim][2p], V^T[dim][2p+1]).
+template <bool kOnlyK>
+__device__ __forceinline__ void tile_commit(const TileRegs& r, GroupLds& s, int tg) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int id = tg + kGroupThreads * i;
+    const int kk = id >> 4, c = id & 15;
+    s.K[kk * 16 + (c ^ (kk & 15))] = r.k[i];
+  }
+  if constexpr (!kOnlyK) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int id = tg + kGroupThreads * i;
       const int pr = id >> 4, c = id & 15;
-      const int na = n0 + 2 * pr, nb = na + 1;
-      u32x4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};
-      if (na < n_end) va = ld16(vbase + slot_of(na) * D + col0 + 8 * c);
-      if (nb < n_end) vb = ld16(vbase + slot_of(nb) * D + col0 + 8 * c);
-      // element j of the chunk is dimension 8c + j; V^T[dim][2pr], V^T[dim][2pr+1]
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t a2 = va[j], b2 = vb[j];
-        Vt[(8 * c + 2 * j) * (kVtStride / 2) + pr] = (a2 & 0xffffu) | (b2 << 16);
-        Vt[(8 * c + 2 * j + 1) * (kVtStride / 2) + pr] = (a2 >> 16) | (b2 & 0xffff0000u);
+        const uint32_t a2 = r.v[i][0][j], b2 = r.v[i][1][j];
+        s.Vt[(8 * c + 2 * j) * (kVtStride / 2) + pr] = (a2 & 0xffffu) | (b2 << 16);
+        s.Vt[(8 * c + 2 * j + 1) * (kVtStride / 2) + pr] = (a2 >> 16) | (b2 & 0xffff0000u);
       }
     }
   }
 }
 
-// One 64-key tile of the online softmax + PV for this lane's row. valid(i, kb) says whether
-// key 16*kb + 4*(l/16) + i of the tile may be attended by this lane's row.
-template <typename Valid>
-__device__ __forceinline__ void attend_tile(TileState& st, const bf16x8 (&qf)[4],
-                                            const u32x4* Ks, const uint32_t* Vt, float scale_log2,
-                                            Valid valid) {
+// One 64-key block of online softmax + PV for the wave's RB row blocks. valid(rb, i, kb):
+// may row block rb's lane row attend key 16*kb + 4*(l/16) + i of the block?
+template <int RB, typename Valid>
+__device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf)[RB][4],
+                                             const GroupLds& s, float scale_log2, Valid valid) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
-  f32x4 s[4];
+  f32x4 sc[RB][4];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
     for (int sd = 0; sd < 4; ++sd) {
-      const bf16x8 kf = as_bf16x8(Ks[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
-      acc = mfma16(kf, qf[sd], acc);
+      const bf16x8 kf = as_bf16x8(s.K[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) sc[rb][kb] = mfma16(kf, qf[rb][sd], sc[rb][kb]);
     }
-    s[kb] = acc;
+  bf16x8 pb[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = valid(rb, i, kb) ? sc[rb][kb][i] * scale_log2 : -INFINITY;
+        sc[rb][kb][i] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = xmax(tmax);
+    const float m_new = fmaxf(st.m[rb], tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // nothing attended yet
+    const float alpha = exp2f(st.m[rb] - m_use);
+    st.m[rb] = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = exp2f(sc[rb][kb][i] - m_use);
+        sc[rb][kb][i] = p;
+        psum += p;
+      }
+    st.l[rb] = st.l[rb] * alpha + psum;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[rb][db] *= alpha;
+    // k-slot (g, j) of PV step ks is key 32ks + 4g + j (j < 4) or 32ks + 16 + 4g + (j - 4)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pb[rb][ks][j] = static_cast<__bf16>(sc[rb][2 * ks][j]);
+        pb[rb][ks][j + 4] = static_cast<__bf16>(sc[rb][2 * ks + 1][j]);
+      }
   }
-  float tmax = -INFINITY;
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = valid(i, kb) ? s[kb][i] * scale_log2 : -INFINITY;
-      s[kb][i] = v;
-      tmax = fmaxf(tmax, v);
-    }
-  tmax = wave_max16x4(tmax);
-  const float m_new = fmaxf(st.m, tmax);
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;  // row with nothing to attend yet
-  const float alpha = exp2f(st.m - m_use);
-  st.m = m_new;
-  float psum = 0.f;
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p = exp2f(s[kb][i] - m_use);
-      s[kb][i] = p;
-      psum += p;
-    }
-  st.l = st.l * alpha + psum;
-#pragma unroll
-  for (int db = 0; db < 8; ++db) st.o[db] *= alpha;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    // k-slot (g, j) of this step is key 32ks + 4g + j (j < 4) or 32ks + 16 + 4g + (j - 4)
-    bf16x8 pb;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pb[j] = static_cast<__bf16>(s[2 * ks][j]);
-      pb[j + 4] = static_cast<__bf16>(s[2 * ks + 1][j]);
-    }
+  for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      const uint32_t* vr = Vt + (16 * db + l16) * (kVtStride / 2);
-      const u32x2 lo = ld8(vr + 16 * ks + 2 * g);
-      const u32x2 hi = ld8(vr + 16 * ks + 8 + 2 * g);
-      st.o[db] = mfma16(as_bf16x8(lo, hi), pb, st.o[db]);
+      const uint32_t* vr = s.Vt + (16 * db + l16) * (kVtStride / 2);
+      const bf16x8 vf = as_bf16x8(ld8(vr + 16 * ks + 2 * g), ld8(vr + 16 * ks + 8 + 2 * g));
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma16(vf, pb[rb][ks], st.o[rb][db]);
     }
-  }
 }
 
-// Column sums over this wavefront's importance rows of S = Q K^T for the 64 keys in LDS.
-// Returns, in every lane, the sum for key 16*kb + (l % 16) of kb = 0..3.
-template <typename Term>
-__device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[4],
-                                            const u32x4* Ks, Term term) {
+// Column sums over the wave's importance rows of S = Q K^T for the 64 keys in LDS:
+// out[kb] (in every lane) = sum over rows of term(rb, i, kb, s) for key 16*kb + (l % 16).
+template <int RB, typename Term>
+__device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[RB][4],
+                                            const GroupLds& s, Term term) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sd = 0; sd < 4; ++sd) {
-      const bf16x8 kf = as_bf16x8(Ks[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
-      acc = mfma16(qf[sd], kf, acc);  // S[row 4g+i][key 16kb + l16]
+      const bf16x8 kf = as_bf16x8(s.K[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma16(qf[rb][sd], kf, acc[rb]);  // S[4g+i][key]
     }
     float cs = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cs += term(i, kb, acc[i]);
-    out[kb] = wave_sum16x4(cs);
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cs += term(rb, i, kb, acc[rb][i]);
+    out[kb] = xsum(cs);
   }
 }
 
-template <bool kVerify>
-__global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
-  __shared__ u32x4 Ks[kTileN * 16];                  // 16 KB
-  __shared__ uint32_t Vt[kHeadDim * kVtStride / 2];  // 17 KB
-  __shared__ float imp_buf[4][kTileN];
-  __shared__ float lse_buf[kMaxRows];
+// One key group of short-row tiles runs two workgroups per CU (registers capped at 256).
+template <int RB, int NG, bool kVerify>
+__global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) void attn_kernel(
+    AttnArgs a) {
+  constexpr int kRows = 64 * RB;
+  __shared__ __align__(16) uint8_t smem[NG * sizeof(GroupLds)];
+  __shared__ float imp_buf[NG][4][kTileN];
+  __shared__ float lse_buf[kRows];
+  static_assert(sizeof(float) * kRows * (kHeadDim + 2) <= NG * sizeof(GroupLds) || NG == 1,
+                "combine area must fit in the key-group buffers");
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
+  const int grp = wave >> 2, wr = wave & 3, tg = tid & (kGroupThreads - 1);
   const int l16 = lane & 15, g = lane >> 4;
+  GroupLds& lds = reinterpret_cast<GroupLds*>(smem)[grp];
   const int h = blockIdx.y;
   const int64_t D = a.d_model;
   const int col0 = h * kHeadDim;
@@ -216,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     k_end = vb[1];
     row0 = vb[2];
     n_rows = vb[3] - vb[2];
-    // Out-of-range entries (rejected by the host validator) degrade to an empty range.
+    // out-of-range entries (rejected by the host validator) degrade to an empty range
     if (k_begin < 0 || k_end > a.n_keys) k_end = k_begin;
     if (row0 < 0 || int64_t(row0) + n_rows > a.n_q_rows) n_rows = 0;
     if (n_rows > a.block_rows) n_rows = a.block_rows;  // mask rows hold block_rows columns
@@ -235,24 +282,28 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
     if (roff < 0 || int64_t(roff) + (n_rows > 0 ? n_rows : 0) > a.n_row_idx) n_rows = 0;
   }
-  n_rows = n_rows < kMaxRows ? n_rows : kMaxRows;
+  if (n_rows > kRows) n_rows = kRows;
   if (n_rows < 0) n_rows = 0;
   if (n_imp > n_rows) n_imp = n_rows;
+  if (k_end < k_begin) k_end = k_begin;
 
-  // This lane's query row (B operand of S^T, A operand of S).
-  const int rr = wave * 16 + l16;
-  const bool row_ok = rr < n_rows;
-  int64_t qrow = 0;
-  if (row_ok) {
-    qrow = kVerify ? int64_t(row0) + rr : int64_t(a.row_idx[roff + rr]);
-    if (qrow < 0 || qrow >= a.n_q_rows) qrow = -1;
-  }
-  bf16x8 qf[4];
+  // The lane's query rows: row block id = wr * RB + rb covers rows 16 * id .. 16 * id + 15.
+  int64_t qrow[RB];
+  bf16x8 qf[RB][4];
 #pragma unroll
-  for (int sd = 0; sd < 4; ++sd) {
-    u32x4 v = {0, 0, 0, 0};
-    if (row_ok && qrow >= 0) v = ld16(a.q + qrow * D + col0 + 32 * sd + 8 * g);
-    qf[sd] = as_bf16x8(v);
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = 16 * (wr * RB + rb) + l16;
+    qrow[rb] = -1;
+    if (r < n_rows) {
+      const int64_t q = kVerify ? int64_t(row0) + r : int64_t(a.row_idx[roff + r]);
+      if (q >= 0 && q < a.n_q_rows) qrow[rb] = q;
+    }
+#pragma unroll
+    for (int sd = 0; sd < 4; ++sd) {
+      u32x4 v = {0, 0, 0, 0};
+      if (qrow[rb] >= 0) v = ld16(a.q + qrow[rb] * D + col0 + 32 * sd + 8 * g);
+      qf[rb][sd] = as_bf16x8(v);
+    }
   }
 
   const int pl = a.page_log2;
@@ -269,132 +320,229 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     return (s >= 0 && s < n_slots) ? s : 0;  // the host validators reject such tables
   };
 
-  TileState st;
-  st.m = -INFINITY;
-  st.l = 0.f;
+  RowState<RB> st;
 #pragma unroll
-  for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < RB; ++rb) {
+    st.m[rb] = -INFINITY;
+    st.l[rb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
   const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
-  const int imp_waves = (n_imp + 15) >> 4;
+  const bool wave_imp = 16 * RB * wr < n_imp;
+  const int imp_waves = (n_imp + 16 * RB - 1) / (16 * RB);
   float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
 
-  // Writes the importance sums of the previous tile (imp_buf) to imp_part. Call between a
-  // barrier that follows the imp_buf writes and the next imp_buf write.
+  // Block scheduling: the tile's 64-key blocks are split into NG contiguous runs of
+  // per_grp blocks; every group makes per_grp passes so barriers stay uniform.
+  const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
+  const int per_grp = (n_blk + NG - 1) / NG;
+  const int blk0 = grp * per_grp;
+  const int blk_end = min(n_blk, blk0 + per_grp);
+
+  // Writes one group's importance sums of a finished block to imp_part. Called between a
+  // barrier that follows the imp_buf writes and the group's next imp_buf write.
   auto flush_imp = [&](int n0) {
-    if (tid < kTileN) {
-      const int n = n0 + tid;
+    if (tg < kTileN) {
+      const int n = n0 + tg;
       if (n < k_end) {
         float sum = 0.f;
-        for (int w = 0; w < imp_waves; ++w) sum += imp_buf[w][tid];
+        for (int w = 0; w < imp_waves; ++w) sum += imp_buf[grp][w][tg];
         imp_out[slot_of(n)] = sum;
       }
     }
   };
 
-  int prev_n0 = -1;
-  for (int n0 = k_begin; n0 < k_end; n0 += kTileN) {
-    __syncthreads();  // LDS tile (and imp_buf) of the previous iteration is consumed
-    if (imp_raw && prev_n0 >= 0) flush_imp(prev_n0);
-    load_kv_tile<false>(Ks, Vt, a.k, a.v, D, col0, n0, k_end, slot_of);
+  TileRegs regs;
+  if (blk0 < blk_end)
+    tile_issue<false>(regs, tg, a.k, a.v, D, col0, k_begin + kTileN * blk0, k_end, slot_of);
+  for (int i = 0; i < per_grp; ++i) {
+    const int blk = blk0 + i;
+    const bool have = blk < blk_end;
+    const int n0 = k_begin + kTileN * blk;
+    __syncthreads();  // the group's LDS block and imp_buf have been consumed
+    if (imp_raw && have && i > 0) flush_imp(n0 - kTileN);
+    if (have) {
+      tile_commit<false>(regs, lds, tg);
+      if (blk + 1 < blk_end)
+        tile_issue<false>(regs, tg, a.k, a.v, D, col0, n0 + kTileN, k_end, slot_of);
+    }
     __syncthreads();
-    const int n_left = k_end - n0;
-    attend_tile(st, qf, Ks, Vt, a.scale_log2, [&](int i, int kb) {
-      return 16 * kb + 4 * g + i < n_left;
-    });
-    if (imp_raw && wave < imp_waves) {
-      float cs[4];
-      column_sums(cs, qf, Ks, [&](int i, int kb, float s) {
-        return (wave * 16 + 4 * g + i) < n_imp ? s : 0.f;
-      });
-      if (g == 0) {
+    if (have) {
+      const int n_left = k_end - n0;
+      attend_block<RB>(st, qf, lds, a.scale_log2,
+                       [&](int, int ii, int kb) { return 16 * kb + 4 * g + ii < n_left; });
+      if (imp_raw && wave_imp) {
+        float cs[4];
+        column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float s) {
+          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? s : 0.f;
+        });
+        if (g == 0) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) imp_buf[wave][16 * kb + l16] = cs[kb];
+          for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
+        }
       }
     }
-    prev_n0 = n0;
   }
-  if (imp_raw && prev_n0 >= 0) {
+  if (imp_raw) {
     __syncthreads();
-    flush_imp(prev_n0);
+    if (blk_end > blk0) flush_imp(k_begin + kTileN * (blk_end - 1));
   }
 
   if constexpr (kVerify) {
-    // In-block keys: the block's own rows, K/V from the packed verify projections.
+    // In-block keys (the block's own rows from the packed verify projections) under the
+    // block's mask; they belong to the last key group.
     const int br = a.block_rows;
-    const uint8_t* mrow = a.mask + (int64_t(blockIdx.x) * br + (rr < br ? rr : 0)) * br;
     __syncthreads();
-    load_kv_tile<false>(Ks, Vt, a.kblk, a.vblk, D, col0, 0, n_rows,
+    if (grp == NG - 1) {
+      tile_issue<false>(regs, tg, a.kblk, a.vblk, D, col0, 0, n_rows,
                         [&](int n) -> int64_t { return int64_t(row0) + n; });  // rows checked above
+      tile_commit<false>(regs, lds, tg);
+    }
     __syncthreads();
-    attend_tile(st, qf, Ks, Vt, a.scale_log2, [&](int i, int kb) {
-      const int j = 16 * kb + 4 * g + i;
-      return j < n_rows && rr < br && mrow[j] != 0;
-    });
+    if (grp == NG - 1) {
+      attend_block<RB>(st, qf, lds, a.scale_log2, [&](int rb, int ii, int kb) {
+        const int r = 16 * (wr * RB + rb) + l16;
+        const int j = 16 * kb + 4 * g + ii;
+        return j < n_rows && r < br &&
+               a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0;
+      });
+    }
   }
 
-  const float l_tot = wave_sum16x4(st.l);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (row_ok && qrow >= 0) {
-    uint16_t* orow = a.out + qrow * D + col0;
+  // Full row sums in every lane of the row.
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const f32x4 o = st.o[db];
-      u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
-      st8(orow + 16 * db + 4 * g, pk);
+  for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+
+  if constexpr (NG > 1) {
+    // Merge the key groups: group 1 publishes (m, l, O), group 0 rescales and adds.
+    float* comb = reinterpret_cast<float*>(smem);  // [kRows][kHeadDim] then m, l
+    float* comb_m = comb + kRows * kHeadDim;
+    float* comb_l = comb_m + kRows;
+    __syncthreads();
+    if (grp == 1) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * (wr * RB + rb) + l16;
+        if (g == 0) {
+          comb_m[r] = st.m[rb];
+          comb_l[r] = st.l[rb];
+        }
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+          *reinterpret_cast<f32x4*>(comb + r * kHeadDim + 16 * db + 4 * g) = st.o[rb][db];
+      }
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * (wr * RB + rb) + l16;
+        const float m1 = comb_m[r], l1 = comb_l[r];
+        const float m = fmaxf(st.m[rb], m1);
+        const float mu = m == -INFINITY ? 0.f : m;
+        const float a0 = exp2f(st.m[rb] - mu), a1 = exp2f(m1 - mu);
+        st.m[rb] = m;
+        st.l[rb] = st.l[rb] * a0 + l1 * a1;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(comb + r * kHeadDim + 16 * db + 4 * g);
+          st.o[rb][db] = st.o[rb][db] * a0 + o1 * a1;
+        }
+      }
+    }
+  }
+
+  if (grp == 0) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (qrow[rb] < 0) continue;
+      const float inv = st.l[rb] > 0.f ? 1.f / st.l[rb] : 0.f;
+      uint16_t* orow = a.out + qrow[rb] * D + col0;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const f32x4 o = st.o[rb][db];
+        const u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+        st8(orow + 16 * db + 4 * g, pk);
+      }
     }
   }
 
   if (imp_soft) {
     // Second pass over K for the importance rows: sum_r exp2(scale_log2 * s - lse2_r).
-    if (g == 0) lse_buf[rr] = (l_tot > 0.f) ? st.m + log2f(l_tot) : INFINITY;
-    __syncthreads();
-    float lse_r[4];
+    if (grp == 0 && g == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lse_r[i] = lse_buf[wave * 16 + 4 * g + i];
-    prev_n0 = -1;
-    for (int n0 = k_begin; n0 < k_end; n0 += kTileN) {
+      for (int rb = 0; rb < RB; ++rb)
+        lse_buf[16 * (wr * RB + rb) + l16] =
+            st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
+    }
+    __syncthreads();
+    float lse_r[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
+    if (blk0 < blk_end)
+      tile_issue<true>(regs, tg, a.k, a.v, D, col0, k_begin + kTileN * blk0, k_end, slot_of);
+    for (int i = 0; i < per_grp; ++i) {
+      const int blk = blk0 + i;
+      const bool have = blk < blk_end;
+      const int n0 = k_begin + kTileN * blk;
       __syncthreads();
-      if (prev_n0 >= 0) flush_imp(prev_n0);
-      load_kv_tile<true>(Ks, Vt, a.k, a.v, D, col0, n0, k_end, slot_of);
+      if (have && i > 0) flush_imp(n0 - kTileN);
+      if (have) {
+        tile_commit<true>(regs, lds, tg);
+        if (blk + 1 < blk_end)
+          tile_issue<true>(regs, tg, a.k, a.v, D, col0, n0 + kTileN, k_end, slot_of);
+      }
       __syncthreads();
-      if (wave < imp_waves) {
+      if (have && wave_imp) {
         float cs[4];
-        column_sums(cs, qf, Ks, [&](int i, int kb, float s) {
-          return (wave * 16 + 4 * g + i) < n_imp ? exp2f(s * a.scale_log2 - lse_r[i]) : 0.f;
+        column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float s) {
+          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? exp2f(s * a.scale_log2 - lse_r[rb][ii])
+                                                          : 0.f;
         });
         if (g == 0) {
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) imp_buf[wave][16 * kb + l16] = cs[kb];
+          for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
         }
       }
-      prev_n0 = n0;
     }
-    if (prev_n0 >= 0) {
-      __syncthreads();
-      flush_imp(prev_n0);
-    }
+    __syncthreads();
+    if (blk_end > blk0) flush_imp(k_begin + kTileN * (blk_end - 1));
   }
 }
 
-// scores[slot] += scale * sum_h imp_part[h][slot] over the keys of each importance tile.
+// scores[slot] += scale * sum_h imp_part[h][slot] over the keys of each importance tile;
+// blockIdx.y = work item, blockIdx.x strides over its keys.
 __global__ __launch_bounds__(256) void imp_accumulate_kernel(
     const float* __restrict__ part, int n_heads, int64_t n_slots,
     const int32_t* __restrict__ page_table, int n_seq, int max_pages, int page_log2,
     const int32_t* __restrict__ work, float scale, float* __restrict__ scores) {
-  const int32_t* it = work + 8 * blockIdx.x;
+  const int32_t* it = work + 8 * blockIdx.y;
   if (it[5] <= 0) return;
   const int b = it[0], k_begin = it[1], k_end = it[2];
   if (b < 0 || b >= n_seq || k_begin < 0 || int64_t(k_end) > (int64_t(max_pages) << page_log2))
     return;  // rejected by the host validator
   const int32_t* ptab = page_table + int64_t(b) * max_pages;
   const int pmask = (1 << page_log2) - 1;
-  for (int n = k_begin + threadIdx.x; n < k_end; n += blockDim.x) {
+  for (int n = k_begin + blockIdx.x * blockDim.x + threadIdx.x; n < k_end;
+       n += gridDim.x * blockDim.x) {
     const int64_t s = (int64_t(ptab[n >> page_log2]) << page_log2) | (n & pmask);
     if (s < 0 || s >= n_slots) continue;
+    // independent loads, summed in ascending head order
+    float v[8];
     float sum = 0.f;
-    for (int hh = 0; hh < n_heads; ++hh) sum += part[int64_t(hh) * n_slots + s];
+    int hh = 0;
+    for (; hh + 8 <= n_heads; hh += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[int64_t(hh + u) * n_slots + s];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    for (; hh < n_heads; ++hh) sum += part[int64_t(hh) * n_slots + s];
     scores[s] += scale * sum;
   }
 }
@@ -416,6 +564,17 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
+// Two key groups per workgroup while the grid alone would leave CUs idle.
+constexpr int64_t kSplitBelow = 768;
+
+template <int RB, int NG, bool kVerify>
+hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
+  hipLaunchKernelGGL((attn_kernel<RB, NG, kVerify>),
+                     dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
+                     dim3(kGroupThreads * NG), 0, s, args);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace fdl
 
@@ -424,12 +583,14 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
                                    int64_t n_heads, int64_t head_dim,
                                    const int32_t* page_table, int64_t n_seq, int64_t max_pages,
                                    int32_t page_log2, const int32_t* work, int64_t n_work,
-                                   const int32_t* row_idx, int64_t n_row_idx,
+                                   const int32_t* row_idx, int64_t n_row_idx, int32_t tile_rows,
                                    float softmax_scale, void* out, int32_t imp_mode,
                                    float* imp_part, void* stream) {
   using namespace fdl;
   FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
+  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention: tile_rows = %d (64 or 128)", tile_rows);
   if (n_work == 0) return ok();
   int rc = check_common("fdl_block_attention", q, k_cache, v_cache, out, d_model, n_heads,
                         head_dim);
@@ -463,12 +624,20 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   args.max_pages = static_cast<int>(max_pages);
   args.page_log2 = page_log2;
   args.d_model = static_cast<int>(d_model);
+  args.tile_rows = tile_rows;
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
-  hipLaunchKernelGGL(attn_kernel<false>, dim3(static_cast<unsigned>(n_work),
-                                              static_cast<unsigned>(n_heads)),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), args);
-  FDL_HIP_CHECK(hipGetLastError());
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool split = n_work * n_heads < kSplitBelow;
+  hipError_t e;
+  // long-row tiles hold two row blocks per wavefront and run one key group (a second group
+  // would not fit the register file)
+  if (tile_rows == 64)
+    e = split ? launch_attn<1, 2, false>(args, n_work, n_heads, s)
+              : launch_attn<1, 1, false>(args, n_work, n_heads, s);
+  else
+    e = launch_attn<2, 1, false>(args, n_work, n_heads, s);
+  FDL_HIP_CHECK(e);
   return ok();
 }
 
@@ -478,7 +647,7 @@ extern "C" int fdl_importance_accumulate(const float* imp_part, int64_t n_heads,
                                          const int32_t* work, int64_t n_work, float scale,
                                          float* scores, void* stream) {
   using namespace fdl;
-  FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
+  FDL_REQUIRE(n_work >= 0 && n_work < 65536, FDL_ERR_SHAPE,
               "fdl_importance_accumulate: n_work = %lld out of range", (long long)n_work);
   if (n_work == 0) return ok();
   FDL_REQUIRE_PTR(imp_part);
@@ -489,7 +658,7 @@ extern "C" int fdl_importance_accumulate(const float* imp_part, int64_t n_heads,
               "fdl_importance_accumulate: empty dimension");
   FDL_REQUIRE(page_log2 >= 4 && page_log2 <= 12, FDL_ERR_SHAPE,
               "fdl_importance_accumulate: page_log2 = %d outside [4, 12]", page_log2);
-  hipLaunchKernelGGL(imp_accumulate_kernel, dim3(static_cast<unsigned>(n_work)), dim3(256), 0,
+  hipLaunchKernelGGL(imp_accumulate_kernel, dim3(4, static_cast<unsigned>(n_work)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), imp_part, static_cast<int>(n_heads),
                      n_slots, page_table, static_cast<int>(n_seq), static_cast<int>(max_pages),
                      page_log2, work, scale, scores);
@@ -517,7 +686,7 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   FDL_REQUIRE_PTR(mask);
   FDL_REQUIRE((reinterpret_cast<uintptr_t>(k_blk) | reinterpret_cast<uintptr_t>(v_blk)) % 16 == 0,
               FDL_ERR_SHAPE, "fdl_verify_attention: k_blk/v_blk must be 16-byte aligned");
-  FDL_REQUIRE(block_rows >= 1 && block_rows <= kMaxRows, FDL_ERR_UNSUPPORTED,
+  FDL_REQUIRE(block_rows >= 1 && block_rows <= 64, FDL_ERR_UNSUPPORTED,
               "fdl_verify_attention: block_rows = %d outside [1, 64]", block_rows);
   FDL_REQUIRE(n_keys >= 0 && n_keys < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_verify_attention: n_keys out of range");
@@ -540,9 +709,10 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   args.n_keys = n_keys;
   args.d_model = static_cast<int>(d_model);
   args.scale_log2 = softmax_scale * kLog2e;
-  hipLaunchKernelGGL(attn_kernel<true>, dim3(static_cast<unsigned>(n_vblocks),
-                                             static_cast<unsigned>(n_heads)),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), args);
-  FDL_HIP_CHECK(hipGetLastError());
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = n_vblocks * n_heads < kSplitBelow
+                           ? launch_attn<1, 2, true>(args, n_vblocks, n_heads, s)
+                           : launch_attn<1, 1, true>(args, n_vblocks, n_heads, s);
+  FDL_HIP_CHECK(e);
   return ok();
 }

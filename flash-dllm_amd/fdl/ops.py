@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from . import lib as _lib
-from .schedule import AttnPlan
+from .schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, AttnPlan
 
 BF16 = torch.bfloat16
 
@@ -104,12 +104,19 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         if tuple(imp_part.shape) != (n_heads, k_cache.shape[0]):
             raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "imp_part must be [n_heads, n_slots]")
     d_model = q.shape[1]
-    _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-              q.shape[0], k_cache.shape[0], d_model, n_heads, d_model // n_heads,
-              plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
-              plan.page_log2, plan.work_d.data_ptr(), plan.n_work, plan.row_idx_d.data_ptr(),
-              max(int(plan.row_idx.size), 1), float(softmax_scale), out.data_ptr(), int(imp_mode),
-              _ptr(imp_part), _stream(q))
+    stream = _stream(q)
+    n_row_idx = max(int(plan.row_idx.size), 1)
+    # long-row tiles (the first n_long work items), then short-row tiles
+    for first, count, tile_rows in ((0, plan.n_long, LONG_TILE_ROWS),
+                                    (plan.n_long, plan.n_work - plan.n_long, MAX_TILE_ROWS)):
+        if count == 0:
+            continue
+        _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                  q.shape[0], k_cache.shape[0], d_model, n_heads, d_model // n_heads,
+                  plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
+                  plan.page_log2, plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(),
+                  n_row_idx, tile_rows, float(softmax_scale), out.data_ptr(), int(imp_mode),
+                  _ptr(imp_part), stream)
 
 
 def importance_accumulate(imp_part: torch.Tensor, plan: AttnPlan, scale: float,

@@ -19,7 +19,8 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-MAX_TILE_ROWS = 64
+MAX_TILE_ROWS = 64        # rows per tile of the short-row variant
+LONG_TILE_ROWS = 128      # rows per tile of the long-row (full recompute) variant
 DEFAULT_PAGE_LOG2 = 5  # 32-slot pages
 
 
@@ -42,35 +43,44 @@ def contiguous_page_table(n_seq: int, max_length: int, page_log2: int = DEFAULT_
     return (np.arange(n_seq, dtype=np.int64)[:, None] * per + np.arange(per)[None, :]).astype(np.int32)
 
 
-def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS) -> tuple[np.ndarray, np.ndarray]:
-    """Splits each sequence's rows into tiles of at most `max_rows` rows.
+def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS,
+               long_rows: int = LONG_TILE_ROWS) -> tuple[np.ndarray, np.ndarray, int]:
+    """Splits each sequence's rows into tiles.
 
-    Returns (work int32 [n, 8], row_idx int32). The importance rows of a sequence must fit
-    in its first tile.
+    A sequence with more than `max_rows` rows is cut into tiles of up to `long_rows` rows
+    (the variant with two 16-row blocks per wavefront, for MFMA-bound full recomputes);
+    the others get one tile of up to `max_rows` rows. Returns (work int32 [n, 8],
+    row_idx int32, n_long): the first n_long work items are long-row tiles. Within each
+    class tiles are ordered longest first. The importance rows of a sequence must fit in
+    its first tile.
     """
-    items = []
+    items = [[], []]
     row_chunks = []
     off = 0
     for sq in seqs:
         rows = np.asarray(sq.rows, dtype=np.int32).reshape(-1)
-        if sq.n_imp > max_rows:
-            raise ValueError(f"{sq.n_imp} importance rows do not fit one {max_rows}-row tile")
+        cls = 0 if len(rows) > max_rows else 1
+        step = long_rows if cls == 0 else max_rows
+        if sq.n_imp > step:
+            raise ValueError(f"{sq.n_imp} importance rows do not fit one {step}-row tile")
         if sq.n_imp > len(rows):
             raise ValueError("n_imp exceeds the number of rows")
-        for t0 in range(0, len(rows), max_rows):
-            chunk = rows[t0:t0 + max_rows]
+        for t0 in range(0, len(rows), step):
+            chunk = rows[t0:t0 + step]
             n_imp = sq.n_imp if t0 == 0 else 0
-            items.append((sq.batch, sq.k_begin, sq.k_end, off, len(chunk), n_imp, 0, 0))
+            items[cls].append((sq.batch, sq.k_begin, sq.k_end, off, len(chunk), n_imp, 0, 0))
             row_chunks.append(chunk)
             off += len(chunk)
-    if not items:
-        return np.zeros((0, 8), dtype=np.int32), np.zeros(0, dtype=np.int32)
-    work = np.asarray(items, dtype=np.int32)
+    if not row_chunks:
+        return np.zeros((0, 8), dtype=np.int32), np.zeros(0, dtype=np.int32), 0
     row_idx = np.concatenate(row_chunks).astype(np.int32)
-    # longest first: keys x 16-row groups
-    cost = (work[:, 2].astype(np.int64) - work[:, 1]) * ((work[:, 4].astype(np.int64) + 15) // 16)
-    order = np.argsort(-cost, kind="stable")
-    return np.ascontiguousarray(work[order]), row_idx
+    parts = []
+    for it in items:
+        w = np.asarray(it, dtype=np.int32).reshape(-1, 8)
+        # longest first: keys x 16-row groups
+        cost = (w[:, 2].astype(np.int64) - w[:, 1]) * ((w[:, 4].astype(np.int64) + 15) // 16)
+        parts.append(w[np.argsort(-cost, kind="stable")])
+    return np.ascontiguousarray(np.concatenate(parts)), row_idx, len(items[0])
 
 
 def seqs_from_reference_blocks(masked_blocks: np.ndarray, tracked_blocks: np.ndarray,
@@ -106,6 +116,7 @@ class AttnPlan:
     row_idx: np.ndarray
     page_table: np.ndarray
     page_log2: int
+    n_long: int = 0  # leading work items that are long-row (128-row) tiles
     work_d: torch.Tensor = field(repr=False, default=None)
     row_idx_d: torch.Tensor = field(repr=False, default=None)
     page_table_d: torch.Tensor = field(repr=False, default=None)
@@ -146,9 +157,9 @@ class AttnPlan:
 
 def make_plan(seqs: list[SeqRows], page_table: np.ndarray, page_log2: int = DEFAULT_PAGE_LOG2,
               device=None, max_rows: int = MAX_TILE_ROWS) -> AttnPlan:
-    work, row_idx = build_work(seqs, max_rows)
+    work, row_idx, n_long = build_work(seqs, max_rows)
     plan = AttnPlan(work=work, row_idx=row_idx, page_table=np.ascontiguousarray(page_table, dtype=np.int32),
-                    page_log2=page_log2)
+                    page_log2=page_log2, n_long=n_long)
     if device is not None:
         plan.to(device)
     return plan

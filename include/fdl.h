@@ -16,7 +16,7 @@
  *     [1] k_begin   first logical key position (inclusive)
  *     [2] k_end     last logical key position (exclusive), the reference's seqlen_k
  *     [3] row_off   offset into row_idx of this tile's query rows
- *     [4] n_rows    number of query rows (1..64)
+ *     [4] n_rows    number of query rows (1..tile_rows, see fdl_block_attention)
  *     [5] n_imp     the first n_imp rows of the tile feed the importance scores
  *     [6] reserved  (0)
  *     [7] reserved  (0)
@@ -99,6 +99,8 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *   k_cache, v_cache bf16 [n_slots][d_model]
  *   page_table int32 [n_seq][max_pages]; page size 1 << page_log2 (4 <= page_log2 <= 12)
  *   work     int32 [n_work][8] (see above); row_idx int32 [n_row_idx]
+ *   tile_rows 64 or 128: every work item of the call has at most tile_rows rows; 128 selects
+ *            the variant for long (full-recompute) row sets, 64 the one for short ones
  *   out      bf16 [n_q_rows][d_model]       rows named by row_idx are written
  *   imp_mode FDL_IMP_*; imp_part fp32 [n_heads][n_slots]: for every tile with n_imp > 0,
  *            imp_part[h][slot(n)] = sum over its first n_imp rows r of the head-h term
@@ -112,8 +114,8 @@ int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
                         int64_t head_dim, const int32_t* page_table, int64_t n_seq,
                         int64_t max_pages, int32_t page_log2, const int32_t* work,
                         int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
-                        float softmax_scale, void* out, int32_t imp_mode, float* imp_part,
-                        void* stream);
+                        int32_t tile_rows, float softmax_scale, void* out, int32_t imp_mode,
+                        float* imp_part, void* stream);
 
 /*
  * scores[slot(n)] += scale * sum_{h = 0..n_heads-1} imp_part[h][slot(n)] for every tile

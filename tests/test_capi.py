@@ -51,11 +51,13 @@ def test_launchers_reject_bad_scalars_without_gpu():
     lib.call("fdl_qkv_rope_cache", None, None, None, None, None, None, 0, None, None, 0,
              4096, 32, 128, None, None, None, 0, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128,
-            None, 1, 1, 5, None, 1, None, 1, 0.1, None, 0, None, None)
+            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None)
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_block_attention", None, None, None, 4, 4, 2048, 32, 64,
-            None, 1, 1, 5, None, 1, None, 1, 0.1, None, 0, None, None)
+            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128,
+            None, 1, 1, 5, None, 1, None, 1, 96, 0.1, None, 0, None, None)
     lib.call("fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128, None, 1, 1, 5, None,
-             0, None, 1, 0.1, None, 0, None, None)
+             0, None, 1, 64, 0.1, None, 0, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_rank", None, 10, None, 10, None, 1, 16, None, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32,
             128, None, 0, None, 1, None, 64, 0.1, None, None)
@@ -84,7 +86,8 @@ def test_validate_rows():
 
 def test_validate_work():
     pt = contiguous_page_table(2, 128)
-    work, rows = build_work([SeqRows(0, 100, np.arange(0, 40), 8), SeqRows(1, 128, np.arange(40, 150))])
+    work, rows, n_long = build_work([SeqRows(0, 100, np.arange(0, 40), 8), SeqRows(1, 128, np.arange(40, 150))])
+    assert n_long == 1 and work[0, 4] == 110
     w, wp = _arr(work, np.int32)
     r, rp = _arr(rows, np.int32)
     p, pp = _arr(pt, np.int32)
@@ -96,7 +99,7 @@ def test_validate_work():
     _, bp = _arr(bad, np.int32)
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", bp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 256)
     bad = w.copy()
-    bad[0, 4] = 65  # too many rows in a tile
+    bad[0, 4] = 129  # too many rows in a tile
     _, bp = _arr(bad, np.int32)
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_work", bp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 5, 256)
     _expect(lib.FDL_ERR_SHAPE, "fdl_validate_work", wp, len(w), rp, len(r), 150, pp, 2, pt.shape[1], 3, 256)
