@@ -33,6 +33,11 @@ constexpr int kHeadDim = 128;
 constexpr int kTileN = 64;        // keys per LDS block
 constexpr int kGroupThreads = 256;
 constexpr int kVtStride = 68;     // bf16 per V^T row in LDS (136 B: conflict-free column reads)
+constexpr int kSlotCache = 2048;  // keys per workgroup whose cache slots are staged in LDS
+
+// 2^x on the hardware exponential (v_exp_f32). The softmax arguments are <= 0, so results
+// that would be denormal flush to zero, which is harmless here.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct AttnArgs {
   const uint16_t* q;
@@ -175,14 +180,14 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
     tmax = xmax(tmax);
     const float m_new = fmaxf(st.m[rb], tmax);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // nothing attended yet
-    const float alpha = exp2f(st.m[rb] - m_use);
+    const float alpha = fast_exp2(st.m[rb] - m_use);
     st.m[rb] = m_new;
     float psum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = exp2f(sc[rb][kb][i] - m_use);
+        const float p = fast_exp2(sc[rb][kb][i] - m_use);
         sc[rb][kb][i] = p;
         psum += p;
       }
@@ -244,6 +249,7 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
   __shared__ __align__(16) uint8_t smem[NG * sizeof(GroupLds)];
   __shared__ float imp_buf[NG][4][kTileN];
   __shared__ float lse_buf[kRows];
+  __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
   static_assert(sizeof(float) * kRows * (kHeadDim + 2) <= NG * sizeof(GroupLds) || NG == 1,
                 "combine area must fit in the key-group buffers");
 
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
   const int pmask = (1 << pl) - 1;
   const int32_t* ptab = a.page_table + int64_t(b) * a.max_pages;
   const int64_t n_slots = a.n_slots;
-  auto slot_of = [&](int n) -> int64_t {
+  auto lookup = [&](int n) -> int64_t {
     int64_t s;
     if constexpr (kVerify) {
       s = a.key_slots[n];
@@ -318,6 +324,17 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
       s = (int64_t(ptab[n >> pl]) << pl) | (n & pmask);
     }
     return (s >= 0 && s < n_slots) ? s : 0;  // the host validators reject such tables
+  };
+  // The key -> slot map of the tile's key range is staged in LDS once, so the K/V loads
+  // of a block do not wait on a page-table (or key-list) load first.
+  const bool slots_staged = k_end - k_begin <= kSlotCache && n_slots < (int64_t(1) << 31);
+  if (slots_staged) {
+    for (int i = tid; i < k_end - k_begin; i += kGroupThreads * NG)
+      slot_buf[i] = static_cast<int32_t>(lookup(k_begin + i));
+  }
+  __syncthreads();
+  auto slot_of = [&](int n) -> int64_t {
+    return slots_staged ? int64_t(slot_buf[n - k_begin]) : lookup(n);
   };
 
   RowState<RB> st;
@@ -443,7 +460,7 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
         const float m1 = comb_m[r], l1 = comb_l[r];
         const float m = fmaxf(st.m[rb], m1);
         const float mu = m == -INFINITY ? 0.f : m;
-        const float a0 = exp2f(st.m[rb] - mu), a1 = exp2f(m1 - mu);
+        const float a0 = fast_exp2(st.m[rb] - mu), a1 = fast_exp2(m1 - mu);
         st.m[rb] = m;
         st.l[rb] = st.l[rb] * a0 + l1 * a1;
 #pragma unroll
@@ -501,8 +518,9 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
       if (have && wave_imp) {
         float cs[4];
         column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float s) {
-          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? exp2f(s * a.scale_log2 - lse_r[rb][ii])
-                                                          : 0.f;
+          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
+                     ? fast_exp2(s * a.scale_log2 - lse_r[rb][ii])
+                     : 0.f;
         });
         if (g == 0) {
 #pragma unroll

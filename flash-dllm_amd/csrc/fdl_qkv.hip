@@ -15,7 +15,7 @@
 // (columns 64 + 32*wn + j), so lane l holds both members of pair 32*wn + (l % 32) for
 // the same rows and RoPE is applied in registers before the bf16 stores. The reduction
 // runs in 64-wide steps staged through LDS (double-buffered, XOR-swizzled 16-byte chunks);
-// the next step's global loads are in flight while the current step's MFMAs run.
+// the global loads run kStages steps ahead of the MFMAs in a ring of register sets.
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -28,6 +28,7 @@ constexpr int kBM = 128;  // rows per tile
 constexpr int kBN = 128;  // output columns per tile (one head of one matrix)
 constexpr int kKT = 64;   // reduction step, bf16 elements (8 chunks of 16 B per row)
 constexpr int kThreads = 256;
+constexpr int kStages = 4;  // reduction steps in flight (register ring); even
 
 struct QkvArgs {
   const uint16_t* x;
@@ -54,7 +55,8 @@ struct QkvArgs {
 // logical chunk land on 16 distinct 4-bank groups.
 __device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
 
-__global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a) {
+// Two workgroups per CU (registers capped at 256 per lane).
+__global__ __launch_bounds__(kThreads, 2) void qkv_rope_kernel(QkvArgs a) {
   __shared__ u32x4 As[2][kBM * 8];
   __shared__ u32x4 Bs[2][kBN * 8];
   __shared__ int64_t s_dst[kBM];   // K/V destination row per tile row (-1: skip)
@@ -71,7 +73,6 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a) {
   const int h = ns - mat * a.n_heads;
   const int64_t m0 = int64_t(mt) * kBM;
   const int D = a.d_model;
-  const uint16_t* __restrict__ X = a.x + m0 * D;
   const uint16_t* __restrict__ W = a.w[mat] + int64_t(h) * kHeadDim * D;
 
   if (tid < kBM) {
@@ -92,30 +93,37 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a) {
     s_rope[tid] = rope;
   }
 
-  // Global -> LDS staging: each thread moves 4 chunks of the X tile and 4 of the W tile.
+  // Global -> LDS staging: each thread moves 4 chunks of the X tile and 4 of the W tile
+  // per 64-wide step. kStages steps are in flight in a ring of register sets, so a step's
+  // loads have kStages steps of MFMA work to land before they are written to LDS. Tile
+  // rows past n_rows load row n_rows - 1 instead (their results are never stored): the
+  // loads stay unconditional, which keeps the compiler's memory wait counts exact.
   int ld_row[4], ld_c[4];
-  bool ld_ok[4];
+  const uint16_t* xrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int id = tid + kThreads * i;
     ld_row[i] = id >> 3;
     ld_c[i] = id & 7;
-    ld_ok[i] = (m0 + ld_row[i]) < a.n_rows;
+    const int64_t r = min(m0 + ld_row[i], a.n_rows - 1);
+    xrow[i] = a.x + r * D + 8 * ld_c[i];
   }
-  u32x4 ra[4], rb[4];
-  auto load_tile = [&](int k0) {
+  struct Stage {
+    u32x4 a[4], b[4];
+  };
+  Stage rs[kStages];
+  auto issue = [&](Stage& st, int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t off = int64_t(ld_row[i]) * D + k0 + 8 * ld_c[i];
-      ra[i] = ld_ok[i] ? ld16(X + off) : u32x4{0, 0, 0, 0};
-      rb[i] = ld16(W + off);
+      st.a[i] = ld16(xrow[i] + k0);
+      st.b[i] = ld16(W + int64_t(ld_row[i]) * D + k0 + 8 * ld_c[i]);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto commit = [&](const Stage& st, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      As[buf][swz(ld_row[i], ld_c[i])] = ra[i];
-      Bs[buf][swz(ld_row[i], ld_c[i])] = rb[i];
+      As[buf][swz(ld_row[i], ld_c[i])] = st.a[i];
+      Bs[buf][swz(ld_row[i], ld_c[i])] = st.b[i];
     }
   };
 
@@ -133,13 +141,7 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = D / kKT;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * kKT);
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < kKT / 16; ++ks) {
       const int c = 2 * ks + g;  // this lane's 8 reduction elements of the 16-wide step
@@ -152,8 +154,27 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a) {
       acc[1][0] = mfma32(a1, b0, acc[1][0]);
       acc[1][1] = mfma32(a1, b1, acc[1][1]);
     }
-    if (kt + 1 < nk) store_tile(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Step t is loaded into rs[t % kStages] and written to LDS buffer t & 1 after step t - 1
+  // is computed. Steps past the end re-read the last step (an L2 hit) and are never
+  // committed.
+  const int nk = D / kKT;  // a multiple of kStages (checked on the host)
+  auto step_k0 = [&](int t) { return min(t, nk - 1) * kKT; };
+#pragma unroll
+  for (int st = 0; st < kStages; ++st) issue(rs[st], step_k0(st));
+  commit(rs[0], 0);
+  __syncthreads();
+  issue(rs[0], step_k0(kStages));
+  for (int kt0 = 0; kt0 < nk; kt0 += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+      const int kt = kt0 + j;  // LDS buffer kt & 1 == j & 1 since kStages is even
+      compute(j & 1);
+      if (kt + 1 < nk) commit(rs[(j + 1) % kStages], (j + 1) & 1);
+      __syncthreads();
+      issue(rs[(j + 1) % kStages], step_k0(kt + 1 + kStages));
+    }
   }
 
   // Epilogue: RoPE in registers, bf16 stores straight to Q / the cache rows.
@@ -204,6 +225,9 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
               (long long)d_model, (long long)n_heads);
   FDL_REQUIRE(d_model <= (1 << 16), FDL_ERR_UNSUPPORTED,
               "fdl_qkv_rope_cache: d_model = %lld too large", (long long)d_model);
+  FDL_REQUIRE(d_model % (kKT * kStages) == 0, FDL_ERR_UNSUPPORTED,
+              "fdl_qkv_rope_cache: d_model = %lld is not a multiple of %d", (long long)d_model,
+              kKT * kStages);
   FDL_REQUIRE(kv_packed == 0 || kv_packed == 1, FDL_ERR_SHAPE,
               "fdl_qkv_rope_cache: kv_packed must be 0 or 1");
   FDL_REQUIRE(!kv_packed || n_kv_rows == n_rows, FDL_ERR_SHAPE,
