@@ -98,6 +98,23 @@ def algorithmic_counts(Q: int) -> dict:
     return dict(qkv=(qkv_f, qkv_b), attn=(attn_f, attn_b))
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "single_layer_bf16_hbm_traffic.txt"
+
+
+def measured_traffic() -> dict:
+    """HBM bytes per launch of each kernel, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters scaled by a 100 MiB copy; see the file's header)."""
+    out = {}
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic":
+                out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
 def run_gpu(steps: int, warmup: int, seed: int = 2):
     import torch
     from fdl import lib, ops
@@ -267,6 +284,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-e2e", action="store_true", help="skip the LLaDA-8B decode leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run five 100 MiB device-to-device copies (the reference kernel for "
+                         "scaling the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--e2e-steps", type=int, default=None,
                     help="bound the HIP decode to this many steps (default: run to completion)")
     ap.add_argument("--e2e-torch-steps", type=int, default=24,
@@ -277,6 +297,14 @@ def main() -> int:
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
     r = run_gpu(args.steps, args.warmup)
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(100 * 1024 * 1024, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     Q = r["Q"]
     per = r["per_kernel_us"]
     cnt = algorithmic_counts(Q)
@@ -294,6 +322,9 @@ def main() -> int:
         "importance_rank": {"us": per["importance_rank"]},
     }
     achieved = qkv_f / t_qkv / 1e6
+    traffic = measured_traffic()
+    if "block_attention" in traffic:
+        kernels["block_attention"]["traffic_bytes"] = traffic["block_attention"]
     out = {
         "metric": METRIC,
         "value": round(us_layer, 2),
@@ -315,7 +346,8 @@ def main() -> int:
                    "head_dim": HD},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "qkv_rope_cache"},
+                     "traffic": traffic.get("qkv_rope_cache"), "kernel": "qkv_rope_cache",
+                     "traffic_source": TRAFFIC_FILE.name},
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
     if not args.no_e2e:

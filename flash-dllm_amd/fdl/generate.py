@@ -33,6 +33,7 @@ What differs from the reference, on purpose:
 """
 from __future__ import annotations
 
+import inspect
 import math
 import time
 from dataclasses import dataclass, field
@@ -102,6 +103,16 @@ def _to_dev(a: np.ndarray, device, dtype=None) -> torch.Tensor:
     return t.to(device)
 
 
+def _accepts_logit_rows(model) -> bool:
+    """True if model.forward takes a `logit_rows` argument (this build's model does; the
+    reference's LLaDAModelLM does not)."""
+    try:
+        params = inspect.signature(model.forward).parameters
+    except (TypeError, ValueError):
+        return False
+    return "logit_rows" in params or any(p.kind == p.VAR_KEYWORD for p in params.values())
+
+
 @torch.no_grad()
 def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, responses, n_steps, steps=128,
                              gen_length=128, block_length=128, temperature=0., remasking='low_confidence',
@@ -124,6 +135,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     L = ((max(prompt_lengths) + gen_length + bm) // bn + 1) * bn
     d_model, n_layers, n_heads = cfg.d_model, cfg.n_layers, cfg.n_heads
     stats = stats if stats is not None else DecodeStats()
+    rows_only = rows_only and _accepts_logit_rows(model)
+    row_kw = (lambda rows: {"logit_rows": rows}) if rows_only else (lambda rows: {})
     t_start = time.perf_counter()
 
     x = np.full(B * L, mask_id, dtype=np.int64)
@@ -207,9 +220,9 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         positions = [qpos_d, empty_i32, rope, plan, attn_scores, []]
         lengths = [start_layer, None, mb_t, tb_t, torch.cat([mb_t, tb_t]), active, len(mb), L, bm, bn, None,
                    False]
-        logit_rows = torch.arange(n_masked_rows, device=dev) if rows_only else None
         logits = model(x_query, use_cache=True, lengths=lengths, positions=positions,
-                       logit_rows=logit_rows).logits.squeeze(0)[:n_masked_rows]
+                       **row_kw(torch.arange(n_masked_rows, device=dev))).logits.squeeze(0)
+        logits = logits[:n_masked_rows]
         stats.forwards += 1
         stats.rows += len(qpos)
         p = F.softmax(logits.to(torch.float64), dim=-1)
@@ -289,7 +302,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             lengths = [start_layer, vblocks_d, None, tb_t, None, active, len(mb), L, bm, bn, None, True]
             if len(lr):
                 vlog = model(xq, use_cache=True, lengths=lengths, positions=positions,
-                             logit_rows=_to_dev(lr, dev) if rows_only else None).logits.squeeze(0)
+                             **row_kw(_to_dev(lr, dev))).logits.squeeze(0)
                 if not rows_only:
                     vlog = vlog[_to_dev(lr, dev)]
                 stats.forwards += 1
