@@ -93,29 +93,45 @@ __device__ __forceinline__ float xsum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// Global loads of keys n0 .. n0+63 (K, and V unless kOnlyK) into registers; tg is the
-// thread's index in its key group. Keys at or past n_end load as zeros.
+// Per-thread sources of a 64-key block: K chunk (id & 15) of keys n0 + (id >> 4) for
+// id = tg + 256 i, and V chunk c of the key pair n0 + 2p, n0 + 2p + 1.
+struct TileSrc {
+  const uint16_t* kcol;  // kbase + col0 + 8 * (chunk of this thread's K loads)
+  const uint16_t* vcol;  // vbase + col0 + 8 * (chunk of this thread's V loads)
+  int kkey;              // key offset (within the block) of the first K chunk
+  int vkey;              // key offset of the first V pair
+};
+
+__device__ __forceinline__ TileSrc tile_src(int tg, const uint16_t* kbase, const uint16_t* vbase,
+                                            int col0) {
+  TileSrc t;
+  t.kcol = kbase + col0 + 8 * (tg & 15);
+  t.vcol = vbase + col0 + 8 * (tg & 15);
+  t.kkey = tg >> 4;
+  t.vkey = 2 * (tg >> 4);
+  return t;
+}
+
+// Global loads of keys n0 .. n0+63 (K, and V unless kOnlyK) into registers. Keys at or
+// past n_end re-read key n_end - 1 (they are masked out of the softmax and their V is
+// multiplied by 0), so every load is unconditional: no branches in the loop and exact
+// memory wait counts. n_end > n0 is required.
 template <bool kOnlyK, typename SlotOf>
-__device__ __forceinline__ void tile_issue(TileRegs& r, int tg, const uint16_t* kbase,
-                                           const uint16_t* vbase, int64_t D, int col0, int n0,
+__device__ __forceinline__ void tile_issue(TileRegs& r, const TileSrc& src, int64_t D, int n0,
                                            int n_end, SlotOf slot_of) {
+  const int last = n_end - 1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int id = tg + kGroupThreads * i;
-    const int n = n0 + (id >> 4);
-    r.k[i] = u32x4{0, 0, 0, 0};
-    if (n < n_end) r.k[i] = ld16(kbase + slot_of(n) * D + col0 + 8 * (id & 15));
+    const int n = min(n0 + src.kkey + 16 * i, last);
+    r.k[i] = ld16(src.kcol + slot_of(n) * D);
   }
   if constexpr (!kOnlyK) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int id = tg + kGroupThreads * i;
-      const int na = n0 + 2 * (id >> 4);
-      const int c = id & 15;
-      r.v[i][0] = u32x4{0, 0, 0, 0};
-      r.v[i][1] = u32x4{0, 0, 0, 0};
-      if (na < n_end) r.v[i][0] = ld16(vbase + slot_of(na) * D + col0 + 8 * c);
-      if (na + 1 < n_end) r.v[i][1] = ld16(vbase + slot_of(na + 1) * D + col0 + 8 * c);
+      const int na = min(n0 + src.vkey + 32 * i, last);
+      const int nb = min(n0 + src.vkey + 32 * i + 1, last);
+      r.v[i][0] = ld16(src.vcol + slot_of(na) * D);
+      r.v[i][1] = ld16(src.vcol + slot_of(nb) * D);
     }
   }
 }
@@ -135,11 +151,13 @@ __device__ __forceinline__ void tile_commit(const TileRegs& r, GroupLds& s, int 
     for (int i = 0; i < 2; ++i) {
       const int id = tg + kGroupThreads * i;
       const int pr = id >> 4, c = id & 15;
+      uint32_t* dst = s.Vt + (8 * c) * (kVtStride / 2) + pr;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t a2 = r.v[i][0][j], b2 = r.v[i][1][j];
-        s.Vt[(8 * c + 2 * j) * (kVtStride / 2) + pr] = (a2 & 0xffffu) | (b2 << 16);
-        s.Vt[(8 * c + 2 * j + 1) * (kVtStride / 2) + pr] = (a2 >> 16) | (b2 & 0xffff0000u);
+        // low halves (dimension 8c + 2j) and high halves (8c + 2j + 1) of the two keys
+        dst[(2 * j) * (kVtStride / 2)] = __builtin_amdgcn_perm(b2, a2, 0x05040100u);
+        dst[(2 * j + 1) * (kVtStride / 2)] = __builtin_amdgcn_perm(b2, a2, 0x07060302u);
       }
     }
   }
@@ -147,7 +165,7 @@ __device__ __forceinline__ void tile_commit(const TileRegs& r, GroupLds& s, int 
 
 // One 64-key block of online softmax + PV for the wave's RB row blocks. valid(rb, i, kb):
 // may row block rb's lane row attend key 16*kb + 4*(l/16) + i of the block?
-template <int RB, typename Valid>
+template <int RB, bool kMasked, typename Valid>
 __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf)[RB][4],
                                              const GroupLds& s, float scale_log2, Valid valid) {
   const int lane = threadIdx.x & 63;
@@ -173,7 +191,8 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = valid(rb, i, kb) ? sc[rb][kb][i] * scale_log2 : -INFINITY;
+        float v = sc[rb][kb][i] * scale_log2;
+        if constexpr (kMasked) v = valid(rb, i, kb) ? v : -INFINITY;
         sc[rb][kb][i] = v;
         tmax = fmaxf(tmax, v);
       }
@@ -372,33 +391,46 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
     }
   };
 
-  TileRegs regs;
-  if (blk0 < blk_end)
-    tile_issue<false>(regs, tg, a.k, a.v, D, col0, k_begin + kTileN * blk0, k_end, slot_of);
-  for (int i = 0; i < per_grp; ++i) {
-    const int blk = blk0 + i;
-    const bool have = blk < blk_end;
-    const int n0 = k_begin + kTileN * blk;
-    __syncthreads();  // the group's LDS block and imp_buf have been consumed
-    if (imp_raw && have && i > 0) flush_imp(n0 - kTileN);
-    if (have) {
-      tile_commit<false>(regs, lds, tg);
-      if (blk + 1 < blk_end)
-        tile_issue<false>(regs, tg, a.k, a.v, D, col0, n0 + kTileN, k_end, slot_of);
-    }
-    __syncthreads();
-    if (have) {
-      const int n_left = k_end - n0;
-      attend_block<RB>(st, qf, lds, a.scale_log2,
-                       [&](int, int ii, int kb) { return 16 * kb + 4 * g + ii < n_left; });
-      if (imp_raw && wave_imp) {
-        float cs[4];
-        column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float s) {
-          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? s : 0.f;
-        });
-        if (g == 0) {
+  // Two blocks per key group are in flight in a two-slot register ring: block blk is
+  // loaded into regs[blk & 1], two blocks ahead of its use. The prefetch index is clamped
+  // to the tile's last block so every load is unconditional (exact wait counts); the
+  // clamped extra loads are never committed.
+  TileRegs regs[2];
+  const TileSrc csrc = tile_src(tg, a.k, a.v, col0);
+  const int last_blk = n_blk - 1;
+  auto blk_n0 = [&](int blk) { return k_begin + kTileN * min(blk, last_blk); };
+  if (n_blk > 0) {
+    tile_issue<false>(regs[0], csrc, D, blk_n0(blk0), k_end, slot_of);
+    tile_issue<false>(regs[1], csrc, D, blk_n0(blk0 + 1), k_end, slot_of);
+    for (int i = 0; i < per_grp; i += 2) {
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
+      for (int j = 0; j < 2; ++j) {
+        const int blk = blk0 + i + j;
+        const bool have = i + j < per_grp && blk < blk_end;
+        const int n0 = k_begin + kTileN * blk;
+        __syncthreads();  // the group's LDS block and imp_buf have been consumed
+        if (imp_raw && have && i + j > 0) flush_imp(n0 - kTileN);
+        if (have) tile_commit<false>(regs[j], lds, tg);
+        tile_issue<false>(regs[j], csrc, D, blk_n0(blk + 2), k_end, slot_of);
+        __syncthreads();
+        if (have) {
+          const int n_left = k_end - n0;
+          if (n_left >= kTileN)
+            attend_block<RB, false>(st, qf, lds, a.scale_log2, [](int, int, int) { return true; });
+          else
+            attend_block<RB, true>(st, qf, lds, a.scale_log2, [&](int, int ii, int kb) {
+              return 16 * kb + 4 * g + ii < n_left;
+            });
+          if (imp_raw && wave_imp) {
+            float cs[4];
+            column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float sv) {
+              return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? sv : 0.f;
+            });
+            if (g == 0) {
+#pragma unroll
+              for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
+            }
+          }
         }
       }
     }
@@ -413,14 +445,14 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
     // block's mask; they belong to the last key group.
     const int br = a.block_rows;
     __syncthreads();
-    if (grp == NG - 1) {
-      tile_issue<false>(regs, tg, a.kblk, a.vblk, D, col0, 0, n_rows,
+    if (grp == NG - 1 && n_rows > 0) {
+      tile_issue<false>(regs[0], tile_src(tg, a.kblk, a.vblk, col0), D, 0, n_rows,
                         [&](int n) -> int64_t { return int64_t(row0) + n; });  // rows checked above
-      tile_commit<false>(regs, lds, tg);
+      tile_commit<false>(regs[0], lds, tg);
     }
     __syncthreads();
-    if (grp == NG - 1) {
-      attend_block<RB>(st, qf, lds, a.scale_log2, [&](int rb, int ii, int kb) {
+    if (grp == NG - 1 && n_rows > 0) {
+      attend_block<RB, true>(st, qf, lds, a.scale_log2, [&](int rb, int ii, int kb) {
         const int r = 16 * (wr * RB + rb) + l16;
         const int j = 16 * kb + 4 * g + ii;
         return j < n_rows && r < br &&
@@ -501,30 +533,32 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
-    if (blk0 < blk_end)
-      tile_issue<true>(regs, tg, a.k, a.v, D, col0, k_begin + kTileN * blk0, k_end, slot_of);
-    for (int i = 0; i < per_grp; ++i) {
-      const int blk = blk0 + i;
-      const bool have = blk < blk_end;
-      const int n0 = k_begin + kTileN * blk;
-      __syncthreads();
-      if (have && i > 0) flush_imp(n0 - kTileN);
-      if (have) {
-        tile_commit<true>(regs, lds, tg);
-        if (blk + 1 < blk_end)
-          tile_issue<true>(regs, tg, a.k, a.v, D, col0, n0 + kTileN, k_end, slot_of);
-      }
-      __syncthreads();
-      if (have && wave_imp) {
-        float cs[4];
-        column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float s) {
-          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
-                     ? fast_exp2(s * a.scale_log2 - lse_r[rb][ii])
-                     : 0.f;
-        });
-        if (g == 0) {
+    if (n_blk > 0) {
+      tile_issue<true>(regs[0], csrc, D, blk_n0(blk0), k_end, slot_of);
+      tile_issue<true>(regs[1], csrc, D, blk_n0(blk0 + 1), k_end, slot_of);
+      for (int i = 0; i < per_grp; i += 2) {
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
+        for (int j = 0; j < 2; ++j) {
+          const int blk = blk0 + i + j;
+          const bool have = i + j < per_grp && blk < blk_end;
+          const int n0 = k_begin + kTileN * blk;
+          __syncthreads();
+          if (have && i + j > 0) flush_imp(n0 - kTileN);
+          if (have) tile_commit<true>(regs[j], lds, tg);
+          tile_issue<true>(regs[j], csrc, D, blk_n0(blk + 2), k_end, slot_of);
+          __syncthreads();
+          if (have && wave_imp) {
+            float cs[4];
+            column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float sv) {
+              return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
+                         ? fast_exp2(sv * a.scale_log2 - lse_r[rb][ii])
+                         : 0.f;
+            });
+            if (g == 0) {
+#pragma unroll
+              for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
+            }
+          }
         }
       }
     }
