@@ -36,6 +36,9 @@ HIPCC_FLAGS = [
     # keep the compiler from forming packed fp32 ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per-source additions. The QKV kernels keep their MFMA accumulators in VGPRs: with the
+# accumulators in AGPRs the register allocator shuffles them between loop iterations.
+HIPCC_EXTRA = {"fdl_qkv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 
 
@@ -56,7 +59,8 @@ def _run(cmd: list[str]) -> str:
 def _compile(src: str, check: bool) -> tuple[Path, str]:
     obj = BUILD_DIR / (src + ".o")
     if src.endswith(".hip"):
-        cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [_hipcc(), *HIPCC_FLAGS, *HIPCC_EXTRA.get(src, []), "-c", str(CSRC / src),
+               "-o", str(obj)]
         if check:
             cmd.append("-Rpass-analysis=kernel-resource-usage")
     else:

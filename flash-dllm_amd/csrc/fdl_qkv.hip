@@ -8,14 +8,23 @@
 //   K is rotated the same way; V is not rotated.
 //   Q goes to packed row r; K/V go to cache row slot[r] (or packed row r for verify).
 //
-// Tiling. One workgroup (4 wavefronts) computes a 128-row x 128-column tile whose columns
-// are one head of one of the three matrices, i.e. all 64 RoPE pairs (c, c + 64) of that
-// head. Wavefront (wm, wn) owns rows 64*wm .. 64*wm+63 and pair columns 32*wn .. 32*wn+31;
-// it runs 32x32x16 MFMAs on the low block (columns 32*wn + j) and on the high block
-// (columns 64 + 32*wn + j), so lane l holds both members of pair 32*wn + (l % 32) for
-// the same rows and RoPE is applied in registers before the bf16 stores. The reduction
-// runs in 64-wide steps staged through LDS (double-buffered, XOR-swizzled 16-byte chunks);
-// the global loads run kStages steps ahead of the MFMAs in a ring of register sets.
+// The output columns are handled as RoPE pairs (c, c + 64) of a head: pair p of the
+// 3 * n_heads * 64 pairs is column c = p % 64 of head (p / 64) % n_heads of matrix
+// p / (64 * n_heads). A tile is a block of rows times a block of pairs, and a wavefront
+// computes both members of its pairs, so lane l holds (c, c + 64) of the same rows in the
+// same accumulator slot and RoPE runs in registers before the bf16 stores.
+//
+// Two kernels, chosen by the number of rows:
+//  * qkv_stream_kernel<BM, BP> (up to 1024 rows, decode steps): BM rows x BP pairs per
+//    workgroup, sized so the launch covers the 256 CUs (512 rows: 128 x 96 pairs, one
+//    tile per CU). 16x16x32 MFMAs; the X and W tiles of each 64-wide reduction step are
+//    staged through LDS (double buffer), the step's global loads run kStages steps ahead
+//    in a ring of registers, and the LDS fragment reads of the next half-step overlap the
+//    MFMAs of the current one (fragment double buffer, explicit instruction groups).
+//  * qkv_wide_kernel (longer row counts, full recompute): 128 x 64-pair tiles (one head
+//    of one matrix), 32x32x16 MFMAs, two workgroups per CU.
+#include <type_traits>
+
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -24,9 +33,7 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kHalf = 64;
-constexpr int kBM = 128;  // rows per tile
-constexpr int kBN = 128;  // output columns per tile (one head of one matrix)
-constexpr int kKT = 64;   // reduction step, bf16 elements (8 chunks of 16 B per row)
+constexpr int kKT = 64;  // reduction step, bf16 elements (8 chunks of 16 B per row)
 constexpr int kThreads = 256;
 constexpr int kStages = 4;  // reduction steps in flight (register ring); even
 
@@ -55,49 +62,263 @@ struct QkvArgs {
 // logical chunk land on 16 distinct 4-bank groups.
 __device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
 
-// Two workgroups per CU (registers capped at 256 per lane).
-__global__ __launch_bounds__(kThreads, 2) void qkv_rope_kernel(QkvArgs a) {
-  __shared__ u32x4 As[2][kBM * 8];
-  __shared__ u32x4 Bs[2][kBN * 8];
-  __shared__ int64_t s_dst[kBM];   // K/V destination row per tile row (-1: skip)
-  __shared__ int64_t s_rope[kBM];  // sin/cos row per tile row (-1: skip)
+// Workgroup i runs on XCD i % 8. Renumber so that each XCD gets a contiguous run of tiles
+// (tiles are numbered n-block-major): the m-tiles that share one weight slice then run on
+// one XCD and share its L2.
+__device__ __forceinline__ int xcd_tile(int bid, int n_tiles) {
+  return (n_tiles & 7) == 0 ? (bid & 7) * (n_tiles >> 3) + (bid >> 3) : bid;
+}
 
+// Destination rows of tile rows m0 .. m0 + BM - 1, written by threads 0 .. BM - 1:
+// dst[0] = Q row, dst[1] = K/V row (cache slot, or the packed row), rope = sin/cos row.
+// A row past n_rows, or with an out-of-range slot or rope row, gets -1 (skipped in all
+// three outputs).
+template <int BM>
+__device__ __forceinline__ void tile_rows(const QkvArgs& a, int64_t m0, int64_t (&dst)[2][BM],
+                                          int64_t (&rope)[BM]) {
   const int tid = threadIdx.x;
-  // Workgroup i runs on XCD i % 8. Renumber so that each XCD gets a contiguous run of
-  // tiles: the m-tiles that share one weight slice then run on one XCD and share its L2.
-  int t = blockIdx.x;
-  if ((a.n_tiles & 7) == 0) t = (t & 7) * (a.n_tiles >> 3) + (t >> 3);
-  const int ns = t / a.n_mtiles;  // n-slice = matrix * n_heads + head
-  const int mt = t - ns * a.n_mtiles;
-  const int mat = ns / a.n_heads;
-  const int h = ns - mat * a.n_heads;
-  const int64_t m0 = int64_t(mt) * kBM;
-  const int D = a.d_model;
-  const uint16_t* __restrict__ W = a.w[mat] + int64_t(h) * kHeadDim * D;
-
-  if (tid < kBM) {
+  if (tid < BM) {
     const int64_t r = m0 + tid;
-    int64_t dst = -1, rope = -1;
+    int64_t dq = -1, dkv = -1, rr_ok = -1;
     if (r < a.n_rows) {
-      // A row with an out-of-range slot or rope row is skipped in all three outputs.
       const int64_t s = a.slot[r];
       const int64_t rr = a.rope_row ? a.rope_row[r] : s;
       const bool rope_ok = rr >= 0 && rr < a.n_rope_rows;
       const bool slot_ok = a.kv_packed || (s >= 0 && s < a.n_kv_rows);
       if (rope_ok && slot_ok) {
-        dst = (mat == 0 || a.kv_packed) ? r : s;  // Q is always packed by row
-        rope = rr;
+        dq = r;
+        dkv = a.kv_packed ? r : s;
+        rr_ok = rr;
       }
     }
-    s_dst[tid] = dst;
-    s_rope[tid] = rope;
+    dst[0][tid] = dq;
+    dst[1][tid] = dkv;
+    rope[tid] = rr_ok;
+  }
+}
+
+// Rotates (lo, hi) = (q~_c, q~_{c+64}) of one row and stores the bf16 pair.
+__device__ __forceinline__ void store_pair(const QkvArgs& a, int mat, int64_t dst, int64_t rope,
+                                           int head, int c, float lo, float hi) {
+  if (mat < 2) {
+    const float* sn = a.sin + rope * kHeadDim;
+    const float* cs = a.cos + rope * kHeadDim;
+    const float s1 = sn[c], s2 = sn[c + kHalf], c1 = cs[c], c2 = cs[c + kHalf];
+    const float rlo = lo * c1 - hi * s1;
+    const float rhi = hi * c2 + lo * s2;
+    lo = rlo;
+    hi = rhi;
+  }
+  uint16_t* base = mat == 0 ? a.q_out : (mat == 1 ? a.k_out : a.v_out);
+  uint16_t* d = base + dst * a.d_model + int64_t(head) * kHeadDim;
+  d[c] = f2bf(lo);
+  d[c + kHalf] = f2bf(hi);
+}
+
+// ---------------------------------------------------------------------------------------
+// qkv_stream_kernel: BM rows x BP pairs per workgroup; wavefront (wm, wn) owns rows
+// BM/2 * wm .. + BM/2 and pairs BP/2 * wn .. + BP/2 (low and high columns).
+template <int BM, int BP, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void qkv_stream_kernel(QkvArgs a) {
+  constexpr int kWP = BP / 2;               // pairs per wavefront
+  constexpr int kPB = kWP / 16;             // 16-pair MFMA blocks per wavefront
+  constexpr int kRB = BM / 32;              // 16-row MFMA blocks per wavefront
+  constexpr int kXLd = BM * 8 / kThreads;   // X chunks per thread per step
+  constexpr int kWLd = 2 * BP * 8 / kThreads;  // W chunks per thread per step
+  static_assert(kPB >= 1 && kRB >= 1 && kXLd >= 1 && kWLd >= 1, "tile too small");
+  __shared__ u32x4 As[2][BM * 8];
+  __shared__ u32x4 Bs[2][2 * BP * 8];  // rows 0 .. BP-1: low columns; BP .. 2BP-1: high
+  __shared__ int64_t s_dst[2][BM];
+  __shared__ int64_t s_rope[BM];
+
+  const int tid = threadIdx.x;
+  const int t = xcd_tile(blockIdx.x, a.n_tiles);
+  const int nt = t / a.n_mtiles;
+  const int mt = t - nt * a.n_mtiles;
+  const int64_t m0 = int64_t(mt) * BM;
+  const int D = a.d_model;
+  const int pairs_per_mat = a.n_heads * kHalf;
+  tile_rows<BM>(a, m0, s_dst, s_rope);
+
+  // Global -> LDS staging sources. Tile rows past n_rows load row n_rows - 1 (never
+  // stored), so every load is unconditional and the compiler's wait counts stay exact.
+  const uint16_t* xsrc[kXLd];
+  const uint16_t* wsrc[kWLd];
+  int xdst[kXLd], wdst[kWLd];
+#pragma unroll
+  for (int i = 0; i < kXLd; ++i) {
+    const int id = tid + kThreads * i, row = id >> 3, c = id & 7;
+    const int64_t r = min(m0 + row, a.n_rows - 1);
+    xsrc[i] = a.x + r * D + 8 * c;
+    xdst[i] = swz(row, c);
+  }
+#pragma unroll
+  for (int i = 0; i < kWLd; ++i) {
+    const int id = tid + kThreads * i, row = id >> 3, c = id & 7;
+    const int hlf = row / BP, p = BP * nt + (row - hlf * BP);
+    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
+    wsrc[i] = a.w[mat] + int64_t((rem >> 6) * kHeadDim + (rem & 63) + kHalf * hlf) * D + 8 * c;
+    wdst[i] = swz(row, c);
+  }
+  struct Stage {
+    u32x4 x[kXLd], w[kWLd];
+  };
+  Stage ring[kStages];
+  const int nk = D / kKT;  // a multiple of kStages (checked on the host)
+  // Steps past the end re-read the last step (never committed).
+  auto issue = [&](Stage& st, int kt) {
+    const int k0 = min(kt, nk - 1) * kKT;
+#pragma unroll
+    for (int i = 0; i < kXLd; ++i) st.x[i] = ld16(xsrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < kWLd; ++i) st.w[i] = ld16(wsrc[i] + k0);
+  };
+  auto commit = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int i = 0; i < kXLd; ++i) As[buf][xdst[i]] = st.x[i];
+#pragma unroll
+    for (int i = 0; i < kWLd; ++i) Bs[buf][wdst[i]] = st.w[i];
+  };
+
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  // MFMA operands of one 32-wide half-step ss of a step: lane (l16, g4) takes chunk
+  // 4 * ss + g4 of its row.
+  struct Frag {
+    bf16x8 a[kRB];
+    bf16x8 b[2][kPB];
+  };
+  auto read_frag = [&](Frag& f, int buf, int ss) {
+    const int c = 4 * ss + g4;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+      f.a[rb] = as_bf16x8(As[buf][swz((BM / 2) * wm + 16 * rb + l16, c)]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int pb = 0; pb < kPB; ++pb)
+        f.b[h][pb] = as_bf16x8(Bs[buf][swz(BP * h + kWP * wn + 16 * pb + l16, c)]);
+  };
+  f32x4 acc[kRB][2][kPB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int pb = 0; pb < kPB; ++pb)
+          acc[rb][h][pb] = mfma16(f.a[rb], f.b[h][pb], acc[rb][h][pb]);
+  };
+  // Instruction groups for one half-step: the LDS fragment reads and the LDS writes (first
+  // half) or global loads (second half) are spread between the MFMAs.
+  constexpr int kMfma = 2 * kRB * kPB;
+  constexpr int kMem = kXLd + kWLd;
+  auto interleave = [&](auto mem_mask) {
+    if constexpr (kMfma >= 2 * kMem) {
+#pragma unroll
+      for (int i = 0; i < kMem; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(decltype(mem_mask)::value, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kMfma - 2 * kMem, 0);
+    }
+  };
+
+  Frag f0, f1;
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) {
+    issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  commit(ring[0], 0);
+  __syncthreads();
+  read_frag(f0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(ring[0], kStages);
+  __builtin_amdgcn_sched_barrier(0);
+  // Step kt: f0 holds half-step 0 (read earlier), LDS buffer kt & 1 holds the step, ring
+  // slot (kt + 1) % kStages holds step kt + 1 in registers.
+  for (int kt0 = 0; kt0 < nk; kt0 += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+      const int kt = kt0 + j;
+      const int buf = j & 1;  // kStages is even
+      // half-step 0: read half-step 1, store step kt + 1 to the other buffer (its last
+      // reads were before the previous barrier), MFMAs of half-step 0
+      read_frag(f1, buf, 1);
+      commit(ring[(j + 1) % kStages], buf ^ 1);
+      mma(f0);
+      interleave(std::integral_constant<int, 0x200>{});  // LDS write
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      // half-step 1: read half-step 0 of step kt + 1, refill the ring slot, MFMAs
+      read_frag(f0, buf ^ 1, 0);
+      issue(ring[(j + 1) % kStages], kt + 1 + kStages);
+      mma(f1);
+      interleave(std::integral_constant<int, 0x020>{});  // global load
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
+  // Epilogue: acc[rb][h][pb][i] is row BM/2 * wm + 16 rb + 4 g4 + i, pair
+  // BP * nt + kWP * wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
+#pragma unroll
+  for (int pb = 0; pb < kPB; ++pb) {
+    const int p = BP * nt + kWP * wn + 16 * pb + l16;
+    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = (BM / 2) * wm + 16 * rb + 4 * g4 + i;
+        const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
+        if (dst < 0) continue;
+        store_pair(a, mat, dst, s_rope[row], rem >> 6, rem & 63, acc[rb][0][pb][i],
+                   acc[rb][1][pb][i]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// qkv_wide_kernel: one workgroup (4 wavefronts) computes a 128-row x 128-column tile whose
+// columns are one head of one of the three matrices. Wavefront (wm, wn) owns rows
+// 64*wm .. 64*wm+63 and pair columns 32*wn .. 32*wn+31 with 32x32x16 MFMAs on the low
+// block (columns 32*wn + j) and the high block (64 + 32*wn + j). The reduction runs in
+// 64-wide steps staged through LDS (double-buffered); the global loads run kStages steps
+// ahead of the MFMAs in a ring of register sets.
+constexpr int kWideBM = 128;
+constexpr int kWideBN = 128;
+
+__global__ __launch_bounds__(kThreads, 2) void qkv_wide_kernel(QkvArgs a) {
+  __shared__ u32x4 As[2][kWideBM * 8];
+  __shared__ u32x4 Bs[2][kWideBN * 8];
+  __shared__ int64_t s_dst[2][kWideBM];
+  __shared__ int64_t s_rope[kWideBM];
+
+  const int tid = threadIdx.x;
+  const int t = xcd_tile(blockIdx.x, a.n_tiles);
+  const int ns = t / a.n_mtiles;  // n-slice = matrix * n_heads + head
+  const int mt = t - ns * a.n_mtiles;
+  const int mat = ns / a.n_heads;
+  const int h = ns - mat * a.n_heads;
+  const int64_t m0 = int64_t(mt) * kWideBM;
+  const int D = a.d_model;
+  const uint16_t* __restrict__ W = a.w[mat] + int64_t(h) * kHeadDim * D;
+  tile_rows<kWideBM>(a, m0, s_dst, s_rope);
+
   // Global -> LDS staging: each thread moves 4 chunks of the X tile and 4 of the W tile
-  // per 64-wide step. kStages steps are in flight in a ring of register sets, so a step's
-  // loads have kStages steps of MFMA work to land before they are written to LDS. Tile
-  // rows past n_rows load row n_rows - 1 instead (their results are never stored): the
-  // loads stay unconditional, which keeps the compiler's memory wait counts exact.
+  // per 64-wide step. Tile rows past n_rows load row n_rows - 1 instead (their results are
+  // never stored): the loads stay unconditional, which keeps the compiler's memory wait
+  // counts exact.
   int ld_row[4], ld_c[4];
   const uint16_t* xrow[4];
 #pragma unroll
@@ -157,8 +378,7 @@ __global__ __launch_bounds__(kThreads, 2) void qkv_rope_kernel(QkvArgs a) {
   };
 
   // Step t is loaded into rs[t % kStages] and written to LDS buffer t & 1 after step t - 1
-  // is computed. Steps past the end re-read the last step (an L2 hit) and are never
-  // committed.
+  // is computed. Steps past the end re-read the last step and are never committed.
   const int nk = D / kKT;  // a multiple of kStages (checked on the host)
   auto step_k0 = [&](int t) { return min(t, nk - 1) * kKT; };
 #pragma unroll
@@ -177,31 +397,40 @@ __global__ __launch_bounds__(kThreads, 2) void qkv_rope_kernel(QkvArgs a) {
     }
   }
 
-  // Epilogue: RoPE in registers, bf16 stores straight to Q / the cache rows.
-  uint16_t* __restrict__ dst_base = mat == 0 ? a.q_out : (mat == 1 ? a.k_out : a.v_out);
-  const int p = 32 * wn + l32;  // pair index within the head
+  // Epilogue: acc[rb2][hb][e] is row 64 wm + 32 rb2 + 8 (e / 4) + 4 g + e % 4, pair
+  // 32 wn + l32, low (hb = 0) or high (hb = 1) column.
+  const int p = 32 * wn + l32;
 #pragma unroll
   for (int rb2 = 0; rb2 < 2; ++rb2) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int row = 64 * wm + 32 * rb2 + 8 * (e >> 2) + 4 * g + (e & 3);
-      const int64_t dst = s_dst[row];
+      const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
       if (dst < 0) continue;
-      float lo = acc[rb2][0][e], hi = acc[rb2][1][e];
-      if (mat < 2) {
-        const float* sn = a.sin + s_rope[row] * kHeadDim;
-        const float* cs = a.cos + s_rope[row] * kHeadDim;
-        const float s1 = sn[p], s2 = sn[p + kHalf], c1 = cs[p], c2 = cs[p + kHalf];
-        const float rlo = lo * c1 - hi * s1;
-        const float rhi = hi * c2 + lo * s2;
-        lo = rlo;
-        hi = rhi;
-      }
-      uint16_t* d = dst_base + dst * D + int64_t(h) * kHeadDim;
-      d[p] = f2bf(lo);
-      d[p + kHalf] = f2bf(hi);
+      store_pair(a, mat, dst, s_rope[row], h, p, acc[rb2][0][e], acc[rb2][1][e]);
     }
   }
+}
+
+}  // namespace
+}  // namespace fdl
+
+namespace fdl {
+namespace {
+
+// Launch plan by row count (measured on MI355X at d_model 4096): the widest tiles that
+// still give every CU work. Row counts above 1024 use the two-per-CU 128 x 64-pair tiles.
+struct QkvPlan {
+  void (*kernel)(QkvArgs);
+  int bm;  // rows per tile
+  int bp;  // pairs per tile
+};
+
+QkvPlan qkv_plan(int64_t n_rows) {
+  if (n_rows <= 64) return {qkv_stream_kernel<64, 32, 2>, 64, 32};
+  if (n_rows <= 384) return {qkv_stream_kernel<64, 64, 2>, 64, 64};
+  if (n_rows <= 1024) return {qkv_stream_kernel<128, 96, 1>, 128, 96};
+  return {qkv_wide_kernel, kWideBM, kWideBN / 2};
 }
 
 }  // namespace
@@ -249,8 +478,10 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   FDL_REQUIRE_ALIGNED(wq, 16);
   FDL_REQUIRE_ALIGNED(wk, 16);
   FDL_REQUIRE_ALIGNED(wv, 16);
-  const int64_t n_mtiles = (n_rows + kBM - 1) / kBM;
-  const int64_t n_tiles = n_mtiles * 3 * n_heads;
+  const QkvPlan plan = qkv_plan(n_rows);
+  const int64_t n_pairs = 3 * n_heads * kHalf;  // a multiple of every plan's bp
+  const int64_t n_mtiles = (n_rows + plan.bm - 1) / plan.bm;
+  const int64_t n_tiles = n_mtiles * (n_pairs / plan.bp);
   FDL_REQUIRE(n_tiles < (int64_t(1) << 31), FDL_ERR_UNSUPPORTED,
               "fdl_qkv_rope_cache: %lld rows is too many", (long long)n_rows);
   QkvArgs args;
@@ -273,7 +504,7 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   args.n_mtiles = static_cast<int>(n_mtiles);
   args.n_tiles = static_cast<int>(n_tiles);
   args.kv_packed = kv_packed;
-  hipLaunchKernelGGL(qkv_rope_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(plan.kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), args);
   FDL_HIP_CHECK(hipGetLastError());
   return ok();

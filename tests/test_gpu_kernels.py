@@ -97,22 +97,27 @@ def test_qkv_rope_cache_cfg2_shape():
     assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
 
 
-@pytest.mark.parametrize("Q", [1, 17, 129, 300])
+@pytest.mark.parametrize("Q", [1, 17, 129, 300, 700, 1100])
 def test_qkv_rope_cache_ragged_rows_small_model(Q):
+    """Ragged row counts on a 4-head model; together they cover every tile plan of the
+    kernel (up to 64, 384 and 1024 rows, and above), including tiles whose pair block
+    straddles two of the three matrices."""
     rng = np.random.default_rng(Q)
-    slots = rng.choice(1024, Q, replace=False)
-    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(10 + Q, 4, Q, 1024, slots, theta=10000.0)
+    n_slots = max(1024, 2 * Q)
+    slots = rng.choice(n_slots, Q, replace=False)
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(10 + Q, 4, Q, n_slots, slots, theta=10000.0)
     _close(_np(q), q_ref, what="Q")
     _close(_np(kc)[s], k_ref[s], what="K rows")
     _close(_np(vc)[s], v_ref[s], what="V rows")
-    untouched = np.setdiff1d(np.arange(1024), s)
+    untouched = np.setdiff1d(np.arange(n_slots), s)
     assert np.all(_np(kc)[untouched] == POISON)
 
 
-def test_qkv_packed_verify_mode():
+@pytest.mark.parametrize("Q", [64, 600])
+def test_qkv_packed_verify_mode(Q):
     rng = np.random.default_rng(3)
-    slots = rng.integers(0, 256, 64)  # repeated slots are legal when nothing is scattered
-    q, k, v, q_ref, k_ref, v_ref, _ = _qkv_case(3, 4, 64, 256, slots, kv_packed=True)
+    slots = rng.integers(0, 256, Q)  # repeated slots are legal when nothing is scattered
+    q, k, v, q_ref, k_ref, v_ref, _ = _qkv_case(3, 4, Q, 256, slots, kv_packed=True)
     _close(_np(q), q_ref, what="Q")
     _close(_np(k), k_ref, what="K packed")
     _close(_np(v), v_ref, what="V packed")
