@@ -15,14 +15,16 @@
 // same accumulator slot and RoPE runs in registers before the bf16 stores.
 //
 // Two kernels, chosen by the number of rows:
-//  * qkv_stream_kernel<BM, BP> (up to 1024 rows, decode steps): BM rows x BP pairs per
-//    workgroup, sized so the launch covers the 256 CUs (512 rows: 128 x 96 pairs, one
-//    tile per CU). 16x16x32 MFMAs; the X and W tiles of each 64-wide reduction step are
-//    staged through LDS (double buffer), the step's global loads run kStages steps ahead
-//    in a ring of registers, and the LDS fragment reads of the next half-step overlap the
-//    MFMAs of the current one (fragment double buffer, explicit instruction groups).
-//  * qkv_wide_kernel (longer row counts, full recompute): 128 x 64-pair tiles (one head
-//    of one matrix), 32x32x16 MFMAs, two workgroups per CU.
+//  * qkv_pc_kernel (more than 64 rows): 128 rows x 96 pairs per workgroup (512 rows: one
+//    tile per CU). Eight wavefronts in two roles: four producers move the X and W tiles of
+//    each 64-wide reduction step straight from global memory into LDS (global_load_lds,
+//    three LDS stages in flight), and four consumers run the 16x16x32 MFMAs from LDS. A
+//    consumer never issues a global memory instruction, so it is never held behind the
+//    texture-address queue while its SIMD's MFMA unit waits; a producer shares that SIMD.
+//  * qkv_stream_kernel<BM, BP> (up to 64 rows, weight streaming): 64 rows x 32 pairs per
+//    workgroup so the launch covers the CUs; X and W tiles staged through LDS with the
+//    global loads kStages steps ahead in a ring of registers and the LDS fragment reads of
+//    the next half-step interleaved with the MFMAs of the current one.
 #include <type_traits>
 
 #include "fdl_device.h"
@@ -289,126 +291,180 @@ __global__ __launch_bounds__(kThreads, OCC) void qkv_stream_kernel(QkvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// qkv_wide_kernel: one workgroup (4 wavefronts) computes a 128-row x 128-column tile whose
-// columns are one head of one of the three matrices. Wavefront (wm, wn) owns rows
-// 64*wm .. 64*wm+63 and pair columns 32*wn .. 32*wn+31 with 32x32x16 MFMAs on the low
-// block (columns 32*wn + j) and the high block (64 + 32*wn + j). The reduction runs in
-// 64-wide steps staged through LDS (double-buffered); the global loads run kStages steps
-// ahead of the MFMAs in a ring of register sets.
-constexpr int kWideBM = 128;
-constexpr int kWideBN = 128;
+// qkv_pc_kernel: 128 rows x 96 pairs; consumer wavefront (wm, wn) owns rows 64 wm .. + 64
+// and pairs 48 wn .. + 48 (low and high columns).
+constexpr int kPcBM = 128;
+constexpr int kPcBP = 96;
+constexpr int kPcThreads = 512;
+constexpr int kPcStages = 3;                         // LDS stages
+constexpr int kPcABytes = kPcBM * 128;               // X tile of one step (16 KB)
+constexpr int kPcStageBytes = kPcABytes + 2 * kPcBP * 128;  // + W tile (24 KB)
+constexpr int kPcLoads = kPcStageBytes / 1024 / 4;   // 1 KB loads per producer per step
 
-__global__ __launch_bounds__(kThreads, 2) void qkv_wide_kernel(QkvArgs a) {
-  __shared__ u32x4 As[2][kWideBM * 8];
-  __shared__ u32x4 Bs[2][kWideBN * 8];
-  __shared__ int64_t s_dst[2][kWideBM];
-  __shared__ int64_t s_rope[kWideBM];
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* glb_ptr;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier without the compiler's memory fence; each side waits for exactly the
+// memory operations it must (the fence would drain every outstanding global load).
+__device__ __forceinline__ void barrier_lds_drained() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+__global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
+  constexpr int kWP = kPcBP / 2, kPB = kWP / 16;
+  __shared__ __align__(1024) uint8_t smem[kPcStages * kPcStageBytes];
+  __shared__ int64_t s_dst[2][kPcBM];
+  __shared__ int64_t s_rope[kPcBM];
 
   const int tid = threadIdx.x;
   const int t = xcd_tile(blockIdx.x, a.n_tiles);
-  const int ns = t / a.n_mtiles;  // n-slice = matrix * n_heads + head
-  const int mt = t - ns * a.n_mtiles;
-  const int mat = ns / a.n_heads;
-  const int h = ns - mat * a.n_heads;
-  const int64_t m0 = int64_t(mt) * kWideBM;
+  const int nt = t / a.n_mtiles;
+  const int mt = t - nt * a.n_mtiles;
+  const int64_t m0 = int64_t(mt) * kPcBM;
   const int D = a.d_model;
-  const uint16_t* __restrict__ W = a.w[mat] + int64_t(h) * kHeadDim * D;
-  tile_rows<kWideBM>(a, m0, s_dst, s_rope);
+  const int pairs_per_mat = a.n_heads * kHalf;
+  tile_rows<kPcBM>(a, m0, s_dst, s_rope);
+  // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
+  // wavefront executes only its own role's barriers (both roles execute 1 + nk of them).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const bool producer = wave >= 4;
+  const int pw = wave & 3;
+  const int nk = D / kKT;
 
-  // Global -> LDS staging: each thread moves 4 chunks of the X tile and 4 of the W tile
-  // per 64-wide step. Tile rows past n_rows load row n_rows - 1 instead (their results are
-  // never stored): the loads stay unconditional, which keeps the compiler's memory wait
-  // counts exact.
-  int ld_row[4], ld_c[4];
-  const uint16_t* xrow[4];
+  if (producer) {
+    // Load i of producer pw fills LDS bytes [1024 q, 1024 q + 1024) of the step's tile
+    // (q = 8-row block): lane -> row 8 q + lane / 8, LDS chunk lane % 8, which holds the
+    // row's logical chunk (lane % 8) ^ ((row >> 1) & 7) (the swz() layout). Tile rows past
+    // n_rows re-read row n_rows - 1 (never stored).
+    const uint16_t* src[kPcLoads];
+    int dst_off[kPcLoads];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int id = tid + kThreads * i;
-    ld_row[i] = id >> 3;
-    ld_c[i] = id & 7;
-    const int64_t r = min(m0 + ld_row[i], a.n_rows - 1);
-    xrow[i] = a.x + r * D + 8 * ld_c[i];
-  }
-  struct Stage {
-    u32x4 a[4], b[4];
-  };
-  Stage rs[kStages];
-  auto issue = [&](Stage& st, int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      st.a[i] = ld16(xrow[i] + k0);
-      st.b[i] = ld16(W + int64_t(ld_row[i]) * D + k0 + 8 * ld_c[i]);
+    for (int i = 0; i < kPcLoads; ++i) {
+      const int q = kPcLoads * pw + i;
+      const int row = 8 * q + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      if (row < kPcBM) {
+        src[i] = a.x + min(m0 + row, a.n_rows - 1) * D + 8 * c;
+      } else {
+        const int wr = row - kPcBM, hlf = wr / kPcBP;
+        const int p = kPcBP * nt + (wr - hlf * kPcBP);
+        const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
+        src[i] = a.w[mat] + int64_t((rem >> 6) * kHeadDim + (rem & 63) + kHalf * hlf) * D +
+                 8 * c;
+      }
+      dst_off[i] = 1024 * q;
     }
-  };
-  auto commit = [&](const Stage& st, int buf) {
+    // Steps past the end re-read the last step into a stage nobody reads any more.
+    auto issue = [&](int kt, int stage) {
+      const int k0 = min(kt, nk - 1) * kKT;
+      uint8_t* st = smem + stage * kPcStageBytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      As[buf][swz(ld_row[i], ld_c[i])] = st.a[i];
-      Bs[buf][swz(ld_row[i], ld_c[i])] = st.b[i];
+      for (int i = 0; i < kPcLoads; ++i)
+        __builtin_amdgcn_global_load_lds((glb_ptr)(src[i] + k0), (lds_ptr)(st + dst_off[i]), 16,
+                                         0, 0);
+    };
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+    wait_vmcnt<2 * kPcLoads>();  // step 0 landed
+    barrier_only();
+    int stage = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_vmcnt<kPcLoads>();  // step kt + 1 landed (step kt + 2 may still be in flight)
+      barrier_only();
+      issue(kt + kPcStages, stage);  // this stage's last reads came before the barrier
+      stage = stage == kPcStages - 1 ? 0 : stage + 1;
     }
-  };
-
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, g = lane >> 5;
-  const int arow0 = 64 * wm + l32, arow1 = arow0 + 32;
-  const int bcol0 = 32 * wn + l32, bcol1 = bcol0 + kHalf;
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int ks = 0; ks < kKT / 16; ++ks) {
-      const int c = 2 * ks + g;  // this lane's 8 reduction elements of the 16-wide step
-      const bf16x8 a0 = as_bf16x8(As[buf][swz(arow0, c)]);
-      const bf16x8 a1 = as_bf16x8(As[buf][swz(arow1, c)]);
-      const bf16x8 b0 = as_bf16x8(Bs[buf][swz(bcol0, c)]);
-      const bf16x8 b1 = as_bf16x8(Bs[buf][swz(bcol1, c)]);
-      acc[0][0] = mfma32(a0, b0, acc[0][0]);
-      acc[0][1] = mfma32(a0, b1, acc[0][1]);
-      acc[1][0] = mfma32(a1, b0, acc[1][0]);
-      acc[1][1] = mfma32(a1, b1, acc[1][1]);
-    }
-  };
-
-  // Step t is loaded into rs[t % kStages] and written to LDS buffer t & 1 after step t - 1
-  // is computed. Steps past the end re-read the last step and are never committed.
-  const int nk = D / kKT;  // a multiple of kStages (checked on the host)
-  auto step_k0 = [&](int t) { return min(t, nk - 1) * kKT; };
-#pragma unroll
-  for (int st = 0; st < kStages; ++st) issue(rs[st], step_k0(st));
-  commit(rs[0], 0);
-  __syncthreads();
-  issue(rs[0], step_k0(kStages));
-  for (int kt0 = 0; kt0 < nk; kt0 += kStages) {
-#pragma unroll
-    for (int j = 0; j < kStages; ++j) {
-      const int kt = kt0 + j;  // LDS buffer kt & 1 == j & 1 since kStages is even
-      compute(j & 1);
-      if (kt + 1 < nk) commit(rs[(j + 1) % kStages], (j + 1) & 1);
-      __syncthreads();
-      issue(rs[(j + 1) % kStages], step_k0(kt + 1 + kStages));
-    }
+    wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
+    return;
   }
 
-  // Epilogue: acc[rb2][hb][e] is row 64 wm + 32 rb2 + 8 (e / 4) + 4 g + e % 4, pair
-  // 32 wn + l32, low (hb = 0) or high (hb = 1) column.
-  const int p = 32 * wn + l32;
+  const int wm = pw >> 1, wn = pw & 1;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int sw = (l16 >> 1) & 7;
+  struct Frag {
+    u32x4 a[4];
+    u32x4 b[2][kPB];
+  };
+  // MFMA operands of half-step ss of the step in `stage`: lane (l16, g4) takes logical chunk
+  // 4 ss + g4 of its row.
+  auto read_frag = [&](Frag& f, int stage, int ss) {
+    const u32x4* st = reinterpret_cast<const u32x4*>(smem + stage * kPcStageBytes);
+    const int c = (4 * ss + g4) ^ sw;
 #pragma unroll
-  for (int rb2 = 0; rb2 < 2; ++rb2) {
+    for (int rb = 0; rb < 4; ++rb) f.a[rb] = st[(64 * wm + 16 * rb + l16) * 8 + c];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = 64 * wm + 32 * rb2 + 8 * (e >> 2) + 4 * g + (e & 3);
-      const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
-      if (dst < 0) continue;
-      store_pair(a, mat, dst, s_rope[row], h, p, acc[rb2][0][e], acc[rb2][1][e]);
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int pb = 0; pb < kPB; ++pb)
+        f.b[h][pb] = st[kPcABytes / 16 + (kPcBP * h + kWP * wn + 16 * pb + l16) * 8 + c];
+  };
+  f32x4 acc[4][2][kPB];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int pb = 0; pb < kPB; ++pb)
+          acc[rb][h][pb] = mfma16(as_bf16x8(f.a[rb]), as_bf16x8(f.b[h][pb]), acc[rb][h][pb]);
+  };
+  // one LDS read between two MFMAs
+  auto interleave = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4 + 2 * kPB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8 * kPB - 2 * (4 + 2 * kPB), 0);
+  };
+
+  Frag f0, f1;
+  barrier_lds_drained();  // row metadata stored; step 0 landed
+  read_frag(f0, 0, 0);
+  int stage = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int next = stage == kPcStages - 1 ? 0 : stage + 1;
+    read_frag(f1, stage, 1);
+    mma(f0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_lds_drained();  // step kt + 1 landed; this wave's reads of step kt - 2 done
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(f0, next, 0);
+    mma(f1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    stage = next;
+  }
+
+  // Epilogue: acc[rb][h][pb][i] is row 64 wm + 16 rb + 4 g4 + i, pair
+  // 96 nt + 48 wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
+#pragma unroll
+  for (int pb = 0; pb < kPB; ++pb) {
+    const int p = kPcBP * nt + kWP * wn + 16 * pb + l16;
+    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 64 * wm + 16 * rb + 4 * g4 + i;
+        const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
+        if (dst < 0) continue;
+        store_pair(a, mat, dst, s_rope[row], rem >> 6, rem & 63, acc[rb][0][pb][i],
+                   acc[rb][1][pb][i]);
+      }
   }
 }
 
@@ -418,19 +474,19 @@ __global__ __launch_bounds__(kThreads, 2) void qkv_wide_kernel(QkvArgs a) {
 namespace fdl {
 namespace {
 
-// Launch plan by row count (measured on MI355X at d_model 4096): the widest tiles that
-// still give every CU work. Row counts above 1024 use the two-per-CU 128 x 64-pair tiles.
+// Launch plan by row count (measured on MI355X at d_model 4096): up to 64 rows the
+// projection streams the weights (the narrow tiles give every CU work); above that the
+// producer/consumer kernel's wide tiles keep the MFMAs fed.
 struct QkvPlan {
   void (*kernel)(QkvArgs);
-  int bm;  // rows per tile
-  int bp;  // pairs per tile
+  int bm;       // rows per tile
+  int bp;       // pairs per tile
+  int threads;  // per workgroup
 };
 
 QkvPlan qkv_plan(int64_t n_rows) {
-  if (n_rows <= 64) return {qkv_stream_kernel<64, 32, 2>, 64, 32};
-  if (n_rows <= 384) return {qkv_stream_kernel<64, 64, 2>, 64, 64};
-  if (n_rows <= 1024) return {qkv_stream_kernel<128, 96, 1>, 128, 96};
-  return {qkv_wide_kernel, kWideBM, kWideBN / 2};
+  if (n_rows <= 64) return {qkv_stream_kernel<64, 32, 2>, 64, 32, kThreads};
+  return {qkv_pc_kernel, kPcBM, kPcBP, kPcThreads};
 }
 
 }  // namespace
@@ -504,7 +560,7 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   args.n_mtiles = static_cast<int>(n_mtiles);
   args.n_tiles = static_cast<int>(n_tiles);
   args.kv_packed = kv_packed;
-  hipLaunchKernelGGL(plan.kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(plan.kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(plan.threads), 0,
                      static_cast<hipStream_t>(stream), args);
   FDL_HIP_CHECK(hipGetLastError());
   return ok();
