@@ -6,10 +6,15 @@
 // resolved so that among equal scores the lower slot ranks higher (it sits later in the
 // ascending order), which makes the result a total order.
 //
-// One workgroup per segment. Each entry becomes a 64-bit key
+// One workgroup (1024 threads) per segment. Each entry becomes a 64-bit key
 //   (orderable(score) << 32) | (0xffffffff - slot)
-// whose ascending order is (score ascending, slot descending); the keys are bitonic-sorted
-// in LDS (segment padded to a power of two with all-ones keys, which sort last).
+// whose ascending order is (score ascending, slot descending); the segment is padded to
+// 1024 * R keys with all-ones keys (they sort last) and bitonic-sorted with thread t holding
+// keys t*R .. t*R + R - 1 in registers. Compare-exchange steps whose stride is below R run
+// inside a thread, strides R .. 32R are lane exchanges within a wavefront, and only the
+// strides of 64R and above (10 of the 55 steps for 1024 keys) go through LDS
+// with a workgroup barrier. Sixteen wavefronts per segment hide the latency of the
+// exchange steps.
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -17,7 +22,7 @@ namespace fdl {
 namespace {
 
 constexpr int kThreads = 1024;
-constexpr int kMaxLen = 8192;
+constexpr int kMaxLen = 8192;  // 1024 threads x 8 keys
 
 // Monotone map float -> uint32 (x < y  <=>  ord(x) < ord(y)); -0.0 and +0.0 map together.
 __device__ __forceinline__ uint32_t orderable(float f) {
@@ -26,54 +31,117 @@ __device__ __forceinline__ uint32_t orderable(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), mask);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), mask);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Keeps min or max of (mine, other) for element i of a compare-exchange at stride j within
+// bitonic blocks of size k: the lower element of an ascending pair keeps the minimum.
+__device__ __forceinline__ uint64_t cx(uint64_t mine, uint64_t other, int i, int j, int k) {
+  const bool lower = (i & j) == 0;
+  const bool asc = (i & k) == 0;
+  const bool take_min = lower == asc;
+  return take_min ? (mine < other ? mine : other) : (mine < other ? other : mine);
+}
+
+template <int R>
 __global__ __launch_bounds__(kThreads) void rank_kernel(const float* __restrict__ scores,
                                                         int64_t n_scores, int64_t* slots,
                                                         int64_t n_slot_entries,
                                                         const int32_t* __restrict__ seg,
                                                         int max_len, int64_t* topk_out, int k) {
-  extern __shared__ uint64_t keys[];
+  constexpr int P = kThreads * R;
+  __shared__ uint64_t xbuf[2][P];
   const int s = blockIdx.x;
   const int64_t start = seg[2 * s];
   int len = seg[2 * s + 1];
-  // a segment longer than the LDS sized for max_len (rejected by the host) is left as is
+  // a segment longer than max_len (rejected by the host) is left as is
   if (start < 0 || len < 0 || len > max_len || start + len > n_slot_entries) len = 0;
-  int P = 1;
-  while (P < len) P <<= 1;
   const int tid = threadIdx.x;
-  for (int i = tid; i < P; i += kThreads) {
-    uint64_t key = ~uint64_t(0);
+
+  uint64_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid * R + r;
+    uint64_t kv = ~uint64_t(0);
     if (i < len) {
       const int64_t slot = slots[start + i];
       // an out-of-range slot (rejected by the host) ranks below every real score
       const float sc = (slot >= 0 && slot < n_scores) ? scores[slot] : -INFINITY;
-      key = (uint64_t(orderable(sc)) << 32) | uint64_t(0xffffffffu - uint32_t(slot));
+      kv = (uint64_t(orderable(sc)) << 32) | uint64_t(0xffffffffu - uint32_t(slot));
     }
-    keys[i] = key;
+    key[r] = kv;
   }
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
-      for (int i = tid; i < (P >> 1); i += kThreads) {
-        const int lo = 2 * stride * (i / stride) + (i % stride);
-        const int hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint64_t x = keys[lo], y = keys[hi];
-        if ((x > y) == up) {
-          keys[lo] = y;
-          keys[hi] = x;
+
+  int buf = 0;
+  for (int kk = 2; kk <= P; kk <<= 1) {
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      if (j >= 64 * R) {
+        // partner in another wavefront: exchange through LDS (two buffers, so one barrier
+        // separates a step's reads from the next step's writes)
+#pragma unroll
+        for (int r = 0; r < R; ++r) xbuf[buf][tid * R + r] = key[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int i = tid * R + r;
+          key[r] = cx(key[r], xbuf[buf][i ^ j], i, j, kk);
+        }
+        buf ^= 1;
+      } else if (j >= R) {
+        const int lane_mask = j / R;  // partner lane within the wavefront
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int i = tid * R + r;
+          key[r] = cx(key[r], shfl_xor64(key[r], lane_mask), i, j, kk);
+        }
+      } else {
+        // partner register of the same thread (j < R: unrolled over the possible strides so
+        // that every register index is a constant)
+#pragma unroll
+        for (int jj = R / 2; jj >= 1; jj >>= 1) {
+          if (j != jj) continue;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int rp = r ^ jj;
+            if (rp > r) {
+              const int i = tid * R + r;
+              const uint64_t lo = cx(key[r], key[rp], i, jj, kk);
+              const uint64_t hi = cx(key[rp], key[r], i ^ jj, jj, kk);
+              key[r] = lo;
+              key[rp] = hi;
+            }
+          }
         }
       }
     }
   }
-  __syncthreads();
-  for (int i = tid; i < len; i += kThreads)
-    slots[start + i] = int64_t(0xffffffffu - uint32_t(keys[i] & 0xffffffffu));
-  if (topk_out) {
-    for (int j = tid; j < k; j += kThreads) {
-      topk_out[int64_t(s) * k + j] =
-          j < len ? int64_t(0xffffffffu - uint32_t(keys[len - 1 - j] & 0xffffffffu)) : -1;
+
+  // key[r] is now element tid * R + r of the ascending order
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid * R + r;
+    if (i < len) {
+      const int64_t slot = int64_t(0xffffffffu - uint32_t(key[r] & 0xffffffffu));
+      slots[start + i] = slot;
+      const int j = len - 1 - i;  // rank from the top
+      if (topk_out && j < k) topk_out[int64_t(s) * k + j] = slot;
     }
   }
+  if (topk_out) {
+    for (int j = len + tid; j < k; j += kThreads) topk_out[int64_t(s) * k + j] = -1;
+  }
+}
+
+template <int R>
+hipError_t launch_rank(int64_t n_seg, hipStream_t st, const float* scores, int64_t n_scores,
+                       int64_t* slots, int64_t n_slot_entries, const int32_t* seg, int max_len,
+                       int64_t* topk_out, int k) {
+  hipLaunchKernelGGL(rank_kernel<R>, dim3(static_cast<unsigned>(n_seg)), dim3(kThreads), 0, st,
+                     scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -97,12 +165,17 @@ extern "C" int fdl_importance_rank(const float* scores, int64_t n_scores, int64_
   FDL_REQUIRE(k >= 0, FDL_ERR_SHAPE, "fdl_importance_rank: k = %d < 0", k);
   FDL_REQUIRE(topk_out != nullptr || k == 0, FDL_ERR_NULL,
               "fdl_importance_rank: topk_out is NULL with k = %d", k);
-  int P = 1;
-  while (P < max_len) P <<= 1;
-  const size_t lds = sizeof(uint64_t) * static_cast<size_t>(P);
-  hipLaunchKernelGGL(rank_kernel, dim3(static_cast<unsigned>(n_seg)), dim3(kThreads), lds,
-                     static_cast<hipStream_t>(stream), scores, n_scores, slots, n_slot_entries,
-                     seg, max_len, topk_out, k);
-  FDL_HIP_CHECK(hipGetLastError());
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  const int keys_per_thread = (max_len + kThreads - 1) / kThreads;
+  if (keys_per_thread <= 1)
+    e = launch_rank<1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (keys_per_thread <= 2)
+    e = launch_rank<2>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (keys_per_thread <= 4)
+    e = launch_rank<4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else
+    e = launch_rank<8>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  FDL_HIP_CHECK(e);
   return ok();
 }
