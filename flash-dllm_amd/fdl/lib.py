@@ -87,6 +87,12 @@ SIGNATURES: dict[str, tuple] = {
         _p, _i64, _p, _i64,           # key_slots, n_keys, vblocks, n_vblocks
         _p, _i32, _f32, _p, _p,       # mask, block_rows, softmax_scale, out, stream
     ]),
+    "fdl_rms_norm": (ctypes.c_int, [
+        _p, _p, _p,                   # x, residual, weight
+        _i64, _i64, _f32,             # n_rows, d, eps
+        _p, _p, _p,                   # sum_out, out, stream
+    ]),
+    "fdl_silu_mul": (ctypes.c_int, [_p, _p, _i64, _p, _p]),  # gate, up, n, out, stream
     "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),
     "fdl_validate_work": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i64]),
     "fdl_validate_vblocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i32]),

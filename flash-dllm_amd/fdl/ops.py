@@ -181,3 +181,44 @@ def verify_attention(q: torch.Tensor, k_blk: torch.Tensor, v_blk: torch.Tensor,
               n_heads, d_model // n_heads, key_slots.data_ptr() if key_slots.numel() else None,
               key_slots.numel(), vblocks.data_ptr(), nv, mask.data_ptr(), int(block_rows),
               float(softmax_scale), out.data_ptr(), _stream(q))
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+             sum_out: torch.Tensor | None = None):
+    """RMSLayerNorm of x (or of bf16(x + residual)) times weight (fdl_rms_norm).
+
+    Returns out, or (sum_out, out) when a residual is given."""
+    dev = x.device
+    _need(x, "x", BF16, 2)
+    n_rows, d = x.shape
+    _need(weight, "weight", BF16, 1, dev)
+    if weight.shape[0] != d:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"weight has {weight.shape[0]} entries, expected {d}")
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out, "out", BF16, 2, dev)
+    if residual is not None:
+        _need(residual, "residual", BF16, 2, dev)
+        if residual.shape != x.shape:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "residual shape differs from x")
+        if sum_out is None:
+            sum_out = torch.empty_like(x)
+        _need(sum_out, "sum_out", BF16, 2, dev)
+    _lib.call("fdl_rms_norm", x.data_ptr(), _ptr(residual), weight.data_ptr(), n_rows, d,
+              float(eps), _ptr(sum_out), out.data_ptr(), _stream(x))
+    return out if residual is None else (sum_out, out)
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(silu(gate)) * up) (fdl_silu_mul)."""
+    _need(gate, "gate", BF16)
+    _need(up, "up", BF16, None, gate.device)
+    if up.shape != gate.shape:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "up shape differs from gate")
+    if out is None:
+        out = torch.empty_like(gate)
+    _need(out, "out", BF16, None, gate.device)
+    _lib.call("fdl_silu_mul", gate.data_ptr(), up.data_ptr(), gate.numel(), out.data_ptr(),
+              _stream(gate))
+    return out

@@ -19,8 +19,11 @@ half runs on the hand-written gfx950 kernels behind the C ABI (include/fdl.h):
     fdl_qkv_rope_cache       kv_packed: Q/K/V of the verify rows, cache untouched
     fdl_verify_attention     cache keys through key_pos_flat + in-block keys under attn_mask
 
-The MLP half (attn_out, residual, ff_norm, SiLU-gated MLP, residual; :618-636) stays in
-torch, as in the reference.
+The RMSLayerNorms and the SiLU gate run on fused HIP kernels (fdl_rms_norm, with the
+attention residual add folded into ff_norm's pass, and fdl_silu_mul); the projections of
+the MLP half (attn_out, ff_proj, up_proj, ff_out; :618-636) are plain library GEMMs through
+torch, as in the reference. Norm or activation modules of other kinds run as the modules
+themselves.
 
 positions = [query_pos_flat, key_pos_flat, [sin, cos], info, attn_scores, attn_mask]
 lengths   = [start_layer, query_verify_blocks, query_masked_blocks, query_tracked_blocks,
@@ -75,21 +78,50 @@ def _imp_workspace(n_heads: int, n_slots: int, device) -> torch.Tensor:
     return ws
 
 
+def _rms_params(norm):
+    """(weight, eps) when `norm` is a plain RMSLayerNorm with a bf16 weight and no bias
+    (modeling_llada.py:375-403), else None."""
+    if "RMS" not in type(norm).__name__ or "Gemma" in type(norm).__name__:
+        return None
+    w = getattr(norm, "weight", None)
+    if not isinstance(w, torch.Tensor) or w.dtype != torch.bfloat16 or w.dim() != 1:
+        return None
+    if getattr(norm, "bias", None) is not None or not hasattr(norm, "eps"):
+        return None
+    return w, float(norm.eps)
+
+
+def _identity_dropout(m) -> bool:
+    return isinstance(m, torch.nn.Identity) or (
+        isinstance(m, torch.nn.Dropout) and (m.p == 0.0 or not m.training))
+
+
+def _norm(norm, x: torch.Tensor, checkpoint_fn) -> torch.Tensor:
+    p = _rms_params(norm) if checkpoint_fn is None else None
+    if p is None or x.dtype != torch.bfloat16:
+        return checkpoint_fn(norm, x) if checkpoint_fn is not None else norm(x)
+    return ops.rms_norm(x.contiguous(), p[0], p[1])
+
+
 def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
     """attn_out + residual + SiLU-gated MLP + residual (flash_cache_triton.py:618-638)."""
     att = self.attn_out(att)
-    x = x + self.dropout(att)
-    og_x = x
-    if self._activation_checkpoint_fn is not None:
-        x = self._activation_checkpoint_fn(self.ff_norm, x)
+    ck = self._activation_checkpoint_fn
+    p = _rms_params(self.ff_norm) if ck is None else None
+    if (p is not None and _identity_dropout(self.dropout) and x.dtype == torch.bfloat16
+            and att.dtype == torch.bfloat16):
+        # x + dropout(att) and ff_norm in one pass
+        og_x, x = ops.rms_norm(x.contiguous(), p[0], p[1], residual=att.contiguous())
     else:
-        x = self.ff_norm(x)
+        x = x + self.dropout(att)
+        og_x = x
+        x = ck(self.ff_norm, x) if ck is not None else self.ff_norm(x)
     x, x_up = self.ff_proj(x), self.up_proj(x)
-    if self._activation_checkpoint_fn is not None:
-        x = self._activation_checkpoint_fn(self.act, x)
+    if ck is None and isinstance(self.act, torch.nn.SiLU) and x.dtype == torch.bfloat16:
+        x = ops.silu_mul(x, x_up)
     else:
-        x = self.act(x)
-    x = x * x_up
+        x = ck(self.act, x) if ck is not None else self.act(x)
+        x = x * x_up
     x = self.ff_out(x)
     x = self.dropout(x)
     x = og_x + x
@@ -109,7 +141,7 @@ def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengt
     batch_size = len(active_batch)
     softmax_scale = softmax_scale or (1.0 / math.sqrt(head_dim))
 
-    x_normed = self.attn_norm(x)
+    x_normed = _norm(self.attn_norm, x, None)
     att = torch.empty_like(x)
     q = torch.empty_like(x)
     sin, cos = rotary_emb_pos[0], rotary_emb_pos[1]

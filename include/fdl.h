@@ -170,6 +170,25 @@ int fdl_verify_attention(const void* q, const void* k_blk, const void* v_blk,
  * Host-side validators (host pointers; no GPU needed). They return FDL_ERR_RANGE with a
  * message naming the first offending entry.
  */
+/*
+ * Fused elementwise parts of the block around the hot path (one HBM pass each).
+ *
+ * fdl_rms_norm replaces `x_normed = self.attn_norm(x)` (flash_cache_triton.py:494, the
+ * RMSLayerNorm of modeling_llada.py:389-403) and, with a residual, the sequence
+ * `x = x + att; og_x = x; x = self.ff_norm(x)` (flash_cache_triton.py:618-624):
+ *   s = bf16(x + residual) -> sum_out (residual may be NULL: s = x, sum_out unused)
+ *   out = bf16(weight * bf16(s * rsqrt(mean(s^2) + eps)))
+ *   x, residual, sum_out, out bf16 [n_rows][d]; weight bf16 [d]; d % 8 == 0, d <= 8192.
+ */
+int fdl_rms_norm(const void* x, const void* residual, const void* weight, int64_t n_rows,
+                 int64_t d, float eps, void* sum_out, void* out, void* stream);
+
+/*
+ * fdl_silu_mul replaces `x = self.act(x); x = x * x_up` with the SiLU activation
+ * (flash_cache_triton.py:628-633): out = bf16(bf16(silu(gate)) * up), n elements (n % 8 == 0).
+ */
+int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* out, void* stream);
+
 /* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
  * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
 int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,
