@@ -8,21 +8,27 @@
 // and _flash_verify_attention_fwd (flash_cache_triton.py:341-428): cache keys gathered
 // through a slot list followed by the block's own rows as keys under a boolean mask.
 //
-// Workgroup = one tile (up to 64*RB query rows of one sequence) x one head, split into NG
-// key groups of 4 wavefronts. Group g streams its share of the tile's 64-key blocks
-// through its own LDS buffers (K row-major with XOR-swizzled 16-byte chunks, V transposed
-// with padded rows); the next block's global loads are issued into registers before the
-// current block is computed, so HBM latency overlaps the MFMA work. With NG = 2 a tile
-// has two key streams in flight; the groups' partial (max, sum, O) are merged through
-// LDS at the end (exact: rescaled by exp of the max difference).
+// Workgroup = one tile (up to 64*RB query rows of one sequence) x one head; eight
+// wavefronts in two roles. Four producers move 64-key blocks of K and V from the cache
+// (through the page table or key list) straight into LDS with global_load_lds, four
+// blocks in flight; four consumers run the MFMAs and the online softmax from LDS and never
+// issue a global load in the key loop. One workgroup barrier per block hands a block from
+// producers to consumers and its buffer back.
 //
-// Each wavefront owns RB blocks of 16 query rows and computes S^T = K Q^T with 16x16x32
-// MFMAs, so lane l holds the logits of row l % 16 for keys 4*(l/16) + i of each 16-key
-// block: the online-softmax max and sum need two cross-lane steps (xor 16, xor 32), and
-// the bf16 probabilities are already the B operand of O^T = V^T P^T. The K and V^T
-// fragments read from LDS are shared by the RB row blocks. Importance needs column sums
-// over rows instead, so it uses S = Q K^T (the same registers, operands swapped): 4
-// in-lane adds plus the same two cross-lane steps.
+// LDS layouts. K: key row of 256 B, 16-byte chunk c of key n at chunk c ^ (n & 15), read
+// as the A operand of S^T = K Q^T (ds_read_b128, 16 consecutive keys on 16 distinct bank
+// groups). V: key row of 256 B, chunk c at c ^ ((n & 7) << 1), read transposed as the A
+// operand of O^T = V^T P^T with ds_read_b64_tr_b16: in each 16-lane group, source lane s
+// reads 4 values V[n0 + s/4][d0 + 4 (s%4) ..] and output lane i receives
+// V[n0 .. n0+3][d0 + i], i.e. four keys of one V^T row.
+//
+// Each consumer owns RB blocks of 16 query rows and computes S^T with 16x16x32 MFMAs, so
+// lane l holds the logits of row l % 16 for keys 4*(l/16) + i of each 16-key block: the
+// online-softmax max and sum need two cross-lane steps (xor 16, xor 32), and the bf16
+// probabilities are already the B operand of O^T = V^T P^T. Importance needs column sums
+// over rows instead, so it uses S = Q K^T (operand swap): 4 in-lane adds plus the same two
+// cross-lane steps; the softmax-probability importance runs a second pass over K once the
+// rows' log-sum-exp is known.
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -30,10 +36,17 @@ namespace fdl {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kTileN = 64;        // keys per LDS block
-constexpr int kGroupThreads = 256;
-constexpr int kVtStride = 68;     // bf16 per V^T row in LDS (136 B: conflict-free column reads)
-constexpr int kSlotCache = 2048;  // keys per workgroup whose cache slots are staged in LDS
+constexpr int kTileN = 64;                    // keys per block
+constexpr int kThreads = 512;                 // 4 consumer + 4 producer wavefronts
+constexpr int kStages = 4;                    // LDS blocks in flight
+constexpr int kTileBytes = kTileN * 256;      // one K (or V) block: 16 KB
+constexpr int kStageBytes = 2 * kTileBytes;   // K then V
+constexpr int kDmaPerTile = kTileBytes / 1024 / 4;  // 1 KB loads per producer per tile (4)
+constexpr int kSlotCache = 2048;              // keys per workgroup whose slots are staged
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* glb_ptr;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // 2^x on the hardware exponential (v_exp_f32). The softmax arguments are <= 0, so results
 // that would be denormal flush to zero, which is harmless here.
@@ -67,16 +80,6 @@ struct AttnArgs {
   float scale_log2;  // softmax_scale * log2(e)
 };
 
-struct GroupLds {
-  u32x4 K[kTileN * 16];                   // 16 KB
-  uint32_t Vt[kHeadDim * kVtStride / 2];  // 17 KB
-};
-
-struct TileRegs {
-  u32x4 k[4];
-  u32x4 v[2][2];
-};
-
 template <int RB>
 struct RowState {
   float m[RB];      // running max of the lane's rows (log2 domain)
@@ -93,81 +96,54 @@ __device__ __forceinline__ float xsum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// Per-thread sources of a 64-key block: K chunk (id & 15) of keys n0 + (id >> 4) for
-// id = tg + 256 i, and V chunk c of the key pair n0 + 2p, n0 + 2p + 1.
-struct TileSrc {
-  const uint16_t* kcol;  // kbase + col0 + 8 * (chunk of this thread's K loads)
-  const uint16_t* vcol;  // vbase + col0 + 8 * (chunk of this thread's V loads)
-  int kkey;              // key offset (within the block) of the first K chunk
-  int vkey;              // key offset of the first V pair
-};
-
-__device__ __forceinline__ TileSrc tile_src(int tg, const uint16_t* kbase, const uint16_t* vbase,
-                                            int col0) {
-  TileSrc t;
-  t.kcol = kbase + col0 + 8 * (tg & 15);
-  t.vcol = vbase + col0 + 8 * (tg & 15);
-  t.kkey = tg >> 4;
-  t.vkey = 2 * (tg >> 4);
-  return t;
-}
-
-// Global loads of keys n0 .. n0+63 (K, and V unless kOnlyK) into registers. Keys at or
-// past n_end re-read key n_end - 1 (they are masked out of the softmax and their V is
-// multiplied by 0), so every load is unconditional: no branches in the loop and exact
-// memory wait counts. n_end > n0 is required.
-template <bool kOnlyK, typename SlotOf>
-__device__ __forceinline__ void tile_issue(TileRegs& r, const TileSrc& src, int64_t D, int n0,
-                                           int n_end, SlotOf slot_of) {
-  const int last = n_end - 1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int n = min(n0 + src.kkey + 16 * i, last);
-    r.k[i] = ld16(src.kcol + slot_of(n) * D);
-  }
-  if constexpr (!kOnlyK) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int na = min(n0 + src.vkey + 32 * i, last);
-      const int nb = min(n0 + src.vkey + 32 * i + 1, last);
-      r.v[i][0] = ld16(src.vcol + slot_of(na) * D);
-      r.v[i][1] = ld16(src.vcol + slot_of(nb) * D);
-    }
+// Waits until at most n global loads of this wavefront are outstanding (n a multiple of
+// 4 up to 16, the counts the producer pipeline can have).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
   }
 }
+// Workgroup barrier without the compiler's memory fence (which would drain every
+// outstanding global load); each role waits for exactly what it must first.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void barrier_lds_drained() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
-// Registers -> LDS: K chunk c of key kk at chunk c ^ (kk & 15); V transposed, two keys per
-// 32-bit word (V^T[dim][2p], V^T[dim][2p+1]).
-template <bool kOnlyK>
-__device__ __forceinline__ void tile_commit(const TileRegs& r, GroupLds& s, int tg) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int id = tg + kGroupThreads * i;
-    const int kk = id >> 4, c = id & 15;
-    s.K[kk * 16 + (c ^ (kk & 15))] = r.k[i];
-  }
-  if constexpr (!kOnlyK) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int id = tg + kGroupThreads * i;
-      const int pr = id >> 4, c = id & 15;
-      uint32_t* dst = s.Vt + (8 * c) * (kVtStride / 2) + pr;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t a2 = r.v[i][0][j], b2 = r.v[i][1][j];
-        // low halves (dimension 8c + 2j) and high halves (8c + 2j + 1) of the two keys
-        dst[(2 * j) * (kVtStride / 2)] = __builtin_amdgcn_perm(b2, a2, 0x05040100u);
-        dst[(2 * j + 1) * (kVtStride / 2)] = __builtin_amdgcn_perm(b2, a2, 0x07060302u);
-      }
-    }
-  }
+// K fragment (A operand of S^T = K Q^T): keys 16 kb + l16, d chunk 4 sd + g.
+__device__ __forceinline__ bf16x8 k_frag(const u32x4* kt, int kb, int sd, int l16, int g) {
+  return as_bf16x8(kt[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
+}
+
+// V^T fragment (A operand of O^T = V^T P^T) of PV step ks, d block db: k-slot (g, j) is key
+// 32 ks + 4 g + j (j < 4) or 32 ks + 16 + 4 g + (j - 4); row d = 16 db + l16.
+__device__ __forceinline__ bf16x8 vt_frag(const uint8_t* vt, int ks, int db, int l16, int g) {
+  const int key = 32 * ks + 4 * g + (l16 >> 2);
+  const int d = 16 * db + 4 * (l16 & 3);
+  const int c = d >> 3, half = (d >> 2) & 1;
+  const int off = ((c ^ ((key & 7) << 1)) << 4) + (half << 3);  // (key + 16) & 7 == key & 7
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds_ptr)(vt + key * 256 + off));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds_ptr)(vt + (key + 16) * 256 + off));
+  u32x4 w;
+  w[0] = __builtin_bit_cast(u32x2, lo)[0];
+  w[1] = __builtin_bit_cast(u32x2, lo)[1];
+  w[2] = __builtin_bit_cast(u32x2, hi)[0];
+  w[3] = __builtin_bit_cast(u32x2, hi)[1];
+  return as_bf16x8(w);
 }
 
 // One 64-key block of online softmax + PV for the wave's RB row blocks. valid(rb, i, kb):
 // may row block rb's lane row attend key 16*kb + 4*(l/16) + i of the block?
 template <int RB, bool kMasked, typename Valid>
 __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf)[RB][4],
-                                             const GroupLds& s, float scale_log2, Valid valid) {
+                                             const u32x4* kt, const uint8_t* vt,
+                                             float scale_log2, Valid valid) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
   f32x4 sc[RB][4];
@@ -179,7 +155,7 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
     for (int sd = 0; sd < 4; ++sd) {
-      const bf16x8 kf = as_bf16x8(s.K[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
+      const bf16x8 kf = k_frag(kt, kb, sd, l16, g);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) sc[rb][kb] = mfma16(kf, qf[rb][sd], sc[rb][kb]);
     }
@@ -213,7 +189,6 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
     st.l[rb] = st.l[rb] * alpha + psum;
 #pragma unroll
     for (int db = 0; db < 8; ++db) st.o[rb][db] *= alpha;
-    // k-slot (g, j) of PV step ks is key 32ks + 4g + j (j < 4) or 32ks + 16 + 4g + (j - 4)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -226,18 +201,17 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      const uint32_t* vr = s.Vt + (16 * db + l16) * (kVtStride / 2);
-      const bf16x8 vf = as_bf16x8(ld8(vr + 16 * ks + 2 * g), ld8(vr + 16 * ks + 8 + 2 * g));
+      const bf16x8 vf = vt_frag(vt, ks, db, l16, g);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma16(vf, pb[rb][ks], st.o[rb][db]);
     }
 }
 
-// Column sums over the wave's importance rows of S = Q K^T for the 64 keys in LDS:
-// out[kb] (in every lane) = sum over rows of term(rb, i, kb, s) for key 16*kb + (l % 16).
+// Column sums over the wave's importance rows of S = Q K^T for the 64 keys of a block:
+// out[kb] (in every lane) = sum over rows of term(rb, i, s) for key 16*kb + (l % 16).
 template <int RB, typename Term>
 __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[RB][4],
-                                            const GroupLds& s, Term term) {
+                                            const u32x4* kt, Term term) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -247,7 +221,7 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
     for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sd = 0; sd < 4; ++sd) {
-      const bf16x8 kf = as_bf16x8(s.K[(16 * kb + l16) * 16 + ((4 * sd + g) ^ l16)]);
+      const bf16x8 kf = k_frag(kt, kb, sd, l16, g);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma16(qf[rb][sd], kf, acc[rb]);  // S[4g+i][key]
     }
@@ -255,28 +229,30 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cs += term(rb, i, kb, acc[rb][i]);
+      for (int i = 0; i < 4; ++i) cs += term(rb, i, acc[rb][i]);
     out[kb] = xsum(cs);
   }
 }
 
-// One key group of short-row tiles runs two workgroups per CU (registers capped at 256).
-template <int RB, int NG, bool kVerify>
-__global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) void attn_kernel(
-    AttnArgs a) {
+// Steps of a tile, the same sequence for producers and consumers (one barrier each):
+//   [0, n_blk)          cache blocks, K and V
+//   [n_blk, 2 n_blk)    softmax importance only: the cache blocks again, K only
+//   n_blk               verify only (when the block has rows): the in-block keys
+template <int RB, bool kVerify>
+__global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   constexpr int kRows = 64 * RB;
-  __shared__ __align__(16) uint8_t smem[NG * sizeof(GroupLds)];
-  __shared__ float imp_buf[NG][4][kTileN];
+  __shared__ __align__(1024) uint8_t smem[kStages * kStageBytes];
+  __shared__ float imp_buf[2][4][kTileN];   // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
-  static_assert(sizeof(float) * kRows * (kHeadDim + 2) <= NG * sizeof(GroupLds) || NG == 1,
-                "combine area must fit in the key-group buffers");
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int grp = wave >> 2, wr = wave & 3, tg = tid & (kGroupThreads - 1);
+  // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
+  // wavefront executes only its own role's barriers (both roles execute 2 + n_steps).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const bool producer = wave >= 4;
+  const int wr = wave & 3;
   const int l16 = lane & 15, g = lane >> 4;
-  GroupLds& lds = reinterpret_cast<GroupLds*>(smem)[grp];
   const int h = blockIdx.y;
   const int64_t D = a.d_model;
   const int col0 = h * kHeadDim;
@@ -312,6 +288,93 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
 
+  const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
+  const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
+  const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
+  const bool inblock = kVerify && n_rows > 0;
+  const int n_steps = n_blk * (imp_soft ? 2 : 1) + (inblock ? 1 : 0);
+
+  const int pl = a.page_log2;
+  const int pmask = (1 << pl) - 1;
+  const int32_t* ptab = a.page_table + int64_t(b) * a.max_pages;
+  const int64_t n_slots = a.n_slots;
+  auto lookup = [&](int n) -> int64_t {
+    int64_t s;
+    if constexpr (kVerify) {
+      s = a.key_slots[n];
+    } else {
+      s = (int64_t(ptab[n >> pl]) << pl) | (n & pmask);
+    }
+    return (s >= 0 && s < n_slots) ? s : 0;  // the host validators reject such tables
+  };
+  // The key -> slot map of the tile's key range is staged in LDS once, so the producers'
+  // block loads do not wait on a page-table (or key-list) load first.
+  const bool slots_staged = k_end - k_begin <= kSlotCache && n_slots < (int64_t(1) << 31);
+  auto slot_of = [&](int n) -> int64_t {
+    return slots_staged ? int64_t(slot_buf[n - k_begin]) : lookup(n);
+  };
+
+  if (producer) {
+    const int tp = tid - 256;
+    if (slots_staged) {
+      for (int i = tp; i < k_end - k_begin; i += 256)
+        slot_buf[i] = static_cast<int32_t>(lookup(k_begin + i));
+    }
+    barrier_lds_drained();  // #0: slot map staged
+    // Load i of producer wr fills LDS bytes [1024 q, 1024 q + 1024) of a tile, q = 4 wr + i:
+    // keys 4q .. 4q + 3; lane -> key 4q + lane / 16, LDS chunk lane % 16.
+    const int pc = lane & 15;
+    auto issue = [&](int step, int stage) {
+      const int s = min(step, n_steps - 1);  // steps past the end repeat the last one
+      uint8_t* st = smem + stage * kStageBytes;
+      const bool in_blk = kVerify && inblock && s == n_steps - 1;
+      const bool k_only = !kVerify && s >= n_blk;
+      const int blk = k_only ? s - n_blk : s;
+      const int n0 = k_begin + kTileN * blk;
+#pragma unroll
+      for (int i = 0; i < kDmaPerTile; ++i) {
+        const int q = kDmaPerTile * wr + i;
+        const int key = 4 * q + (lane >> 4);
+        const uint16_t *ks, *vs;
+        if (in_blk) {
+          const int64_t r = int64_t(row0) + min(key, n_rows - 1);  // rows checked above
+          ks = a.kblk + r * D + col0;
+          vs = a.vblk + r * D + col0;
+        } else {
+          const int64_t slot = slot_of(min(n0 + key, k_end - 1));
+          ks = a.k + slot * D + col0;
+          vs = a.v + slot * D + col0;
+        }
+        const int kc = pc ^ (key & 15), vc = pc ^ ((key & 7) << 1);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(ks + 8 * kc), (lds_ptr)(st + 1024 * q), 16,
+                                         0, 0);
+        if (!k_only)
+          __builtin_amdgcn_global_load_lds((glb_ptr)(vs + 8 * vc),
+                                           (lds_ptr)(st + kTileBytes + 1024 * q), 16, 0, 0);
+      }
+    };
+    // loads of one step (K only in the second pass)
+    auto loads = [&](int step) {
+      const int s = min(step, n_steps - 1);
+      return (!kVerify && s >= n_blk) ? kDmaPerTile : 2 * kDmaPerTile;
+    };
+    if (n_steps > 0) {
+      for (int s = 0; s < kStages; ++s) issue(s, s);
+      wait_vmcnt(loads(1) + loads(2) + loads(3));  // step 0 landed
+    }
+    barrier_only();  // #1
+    int stage = 0;
+    for (int s = 0; s < n_steps; ++s) {
+      wait_vmcnt(loads(s + 2) + loads(s + 3));  // step s + 1 landed
+      barrier_only();  // consumers are done with step s
+      issue(s + kStages, stage);
+      stage = stage == kStages - 1 ? 0 : stage + 1;
+    }
+    wait_vmcnt(0);  // no load may still be writing LDS when the workgroup ends
+    return;
+  }
+
+  // ---------------------------------------------------------------- consumers
   // The lane's query rows: row block id = wr * RB + rb covers rows 16 * id .. 16 * id + 15.
   int64_t qrow[RB];
   bf16x8 qf[RB][4];
@@ -330,32 +393,6 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
       qf[rb][sd] = as_bf16x8(v);
     }
   }
-
-  const int pl = a.page_log2;
-  const int pmask = (1 << pl) - 1;
-  const int32_t* ptab = a.page_table + int64_t(b) * a.max_pages;
-  const int64_t n_slots = a.n_slots;
-  auto lookup = [&](int n) -> int64_t {
-    int64_t s;
-    if constexpr (kVerify) {
-      s = a.key_slots[n];
-    } else {
-      s = (int64_t(ptab[n >> pl]) << pl) | (n & pmask);
-    }
-    return (s >= 0 && s < n_slots) ? s : 0;  // the host validators reject such tables
-  };
-  // The key -> slot map of the tile's key range is staged in LDS once, so the K/V loads
-  // of a block do not wait on a page-table (or key-list) load first.
-  const bool slots_staged = k_end - k_begin <= kSlotCache && n_slots < (int64_t(1) << 31);
-  if (slots_staged) {
-    for (int i = tid; i < k_end - k_begin; i += kGroupThreads * NG)
-      slot_buf[i] = static_cast<int32_t>(lookup(k_begin + i));
-  }
-  __syncthreads();
-  auto slot_of = [&](int n) -> int64_t {
-    return slots_staged ? int64_t(slot_buf[n - k_begin]) : lookup(n);
-  };
-
   RowState<RB> st;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -364,147 +401,26 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
 #pragma unroll
     for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-
-  const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
-  const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
   const bool wave_imp = 16 * RB * wr < n_imp;
   const int imp_waves = (n_imp + 16 * RB - 1) / (16 * RB);
   float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
+  float lse_r[RB][4];
 
-  // Block scheduling: the tile's 64-key blocks are split into NG contiguous runs of
-  // per_grp blocks; every group makes per_grp passes so barriers stay uniform.
-  const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
-  const int per_grp = (n_blk + NG - 1) / NG;
-  const int blk0 = grp * per_grp;
-  const int blk_end = min(n_blk, blk0 + per_grp);
-
-  // Writes one group's importance sums of a finished block to imp_part. Called between a
-  // barrier that follows the imp_buf writes and the group's next imp_buf write.
-  auto flush_imp = [&](int n0) {
-    if (tg < kTileN) {
-      const int n = n0 + tg;
+  // Writes the importance sums of the block of step `s` (keys from n0): each consumer
+  // wave sums 16 keys over the waves' partials. Runs after the barrier that follows the
+  // partials' writes and before the barrier after which they are overwritten.
+  auto flush_imp = [&](int s, int n0) {
+    if (l16 == lane) {  // lanes 0..15
+      const int key = 16 * wr + lane;
+      const int n = n0 + key;
       if (n < k_end) {
         float sum = 0.f;
-        for (int w = 0; w < imp_waves; ++w) sum += imp_buf[grp][w][tg];
+        for (int w = 0; w < imp_waves; ++w) sum += imp_buf[s & 1][w][key];
         imp_out[slot_of(n)] = sum;
       }
     }
   };
-
-  // Two blocks per key group are in flight in a two-slot register ring: block blk is
-  // loaded into regs[blk & 1], two blocks ahead of its use. The prefetch index is clamped
-  // to the tile's last block so every load is unconditional (exact wait counts); the
-  // clamped extra loads are never committed.
-  TileRegs regs[2];
-  const TileSrc csrc = tile_src(tg, a.k, a.v, col0);
-  const int last_blk = n_blk - 1;
-  auto blk_n0 = [&](int blk) { return k_begin + kTileN * min(blk, last_blk); };
-  if (n_blk > 0) {
-    tile_issue<false>(regs[0], csrc, D, blk_n0(blk0), k_end, slot_of);
-    tile_issue<false>(regs[1], csrc, D, blk_n0(blk0 + 1), k_end, slot_of);
-    for (int i = 0; i < per_grp; i += 2) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int blk = blk0 + i + j;
-        const bool have = i + j < per_grp && blk < blk_end;
-        const int n0 = k_begin + kTileN * blk;
-        __syncthreads();  // the group's LDS block and imp_buf have been consumed
-        if (imp_raw && have && i + j > 0) flush_imp(n0 - kTileN);
-        if (have) tile_commit<false>(regs[j], lds, tg);
-        tile_issue<false>(regs[j], csrc, D, blk_n0(blk + 2), k_end, slot_of);
-        __syncthreads();
-        if (have) {
-          const int n_left = k_end - n0;
-          if (n_left >= kTileN)
-            attend_block<RB, false>(st, qf, lds, a.scale_log2, [](int, int, int) { return true; });
-          else
-            attend_block<RB, true>(st, qf, lds, a.scale_log2, [&](int, int ii, int kb) {
-              return 16 * kb + 4 * g + ii < n_left;
-            });
-          if (imp_raw && wave_imp) {
-            float cs[4];
-            column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float sv) {
-              return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? sv : 0.f;
-            });
-            if (g == 0) {
-#pragma unroll
-              for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
-            }
-          }
-        }
-      }
-    }
-  }
-  if (imp_raw) {
-    __syncthreads();
-    if (blk_end > blk0) flush_imp(k_begin + kTileN * (blk_end - 1));
-  }
-
-  if constexpr (kVerify) {
-    // In-block keys (the block's own rows from the packed verify projections) under the
-    // block's mask; they belong to the last key group.
-    const int br = a.block_rows;
-    __syncthreads();
-    if (grp == NG - 1 && n_rows > 0) {
-      tile_issue<false>(regs[0], tile_src(tg, a.kblk, a.vblk, col0), D, 0, n_rows,
-                        [&](int n) -> int64_t { return int64_t(row0) + n; });  // rows checked above
-      tile_commit<false>(regs[0], lds, tg);
-    }
-    __syncthreads();
-    if (grp == NG - 1 && n_rows > 0) {
-      attend_block<RB, true>(st, qf, lds, a.scale_log2, [&](int rb, int ii, int kb) {
-        const int r = 16 * (wr * RB + rb) + l16;
-        const int j = 16 * kb + 4 * g + ii;
-        return j < n_rows && r < br &&
-               a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0;
-      });
-    }
-  }
-
-  // Full row sums in every lane of the row.
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
-
-  if constexpr (NG > 1) {
-    // Merge the key groups: group 1 publishes (m, l, O), group 0 rescales and adds.
-    float* comb = reinterpret_cast<float*>(smem);  // [kRows][kHeadDim] then m, l
-    float* comb_m = comb + kRows * kHeadDim;
-    float* comb_l = comb_m + kRows;
-    __syncthreads();
-    if (grp == 1) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int r = 16 * (wr * RB + rb) + l16;
-        if (g == 0) {
-          comb_m[r] = st.m[rb];
-          comb_l[r] = st.l[rb];
-        }
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-          *reinterpret_cast<f32x4*>(comb + r * kHeadDim + 16 * db + 4 * g) = st.o[rb][db];
-      }
-    }
-    __syncthreads();
-    if (grp == 0) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int r = 16 * (wr * RB + rb) + l16;
-        const float m1 = comb_m[r], l1 = comb_l[r];
-        const float m = fmaxf(st.m[rb], m1);
-        const float mu = m == -INFINITY ? 0.f : m;
-        const float a0 = fast_exp2(st.m[rb] - mu), a1 = fast_exp2(m1 - mu);
-        st.m[rb] = m;
-        st.l[rb] = st.l[rb] * a0 + l1 * a1;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          const f32x4 o1 = *reinterpret_cast<const f32x4*>(comb + r * kHeadDim + 16 * db + 4 * g);
-          st.o[rb][db] = st.o[rb][db] * a0 + o1 * a1;
-        }
-      }
-    }
-  }
-
-  if (grp == 0) {
+  auto write_out = [&]() {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       if (qrow[rb] < 0) continue;
@@ -513,58 +429,93 @@ __global__ __launch_bounds__(kGroupThreads * NG, (RB == 1 && NG == 1) ? 2 : 1) v
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         const f32x4 o = st.o[rb][db];
-        const u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+        const u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv),
+                          pack_bf16x2(o[2] * inv, o[3] * inv)};
         st8(orow + 16 * db + 4 * g, pk);
       }
     }
-  }
+  };
 
-  if (imp_soft) {
-    // Second pass over K for the importance rows: sum_r exp2(scale_log2 * s - lse2_r).
-    if (grp == 0 && g == 0) {
+  barrier_only();  // #0
+  barrier_only();  // #1: step 0 landed
+  bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
+  int stage = 0;
+  for (int s = 0; s < n_steps; ++s) {
+    const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
+    const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
+    const bool pass2 = !kVerify && s >= n_blk;
+    const bool in_blk = kVerify && inblock && s == n_steps - 1;
+    const int blk = pass2 ? s - n_blk : s;
+    const int n0 = k_begin + kTileN * blk;
+    if ((imp_raw || imp_soft) && s > 0 && (s - 1 < n_blk ? imp_raw : true))
+      flush_imp(s - 1, k_begin + kTileN * ((s - 1) >= n_blk ? s - 1 - n_blk : s - 1));
+    if (in_blk) {
+      const int br = a.block_rows;
+      attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int rb, int ii, int kb) {
+        const int r = 16 * (wr * RB + rb) + l16;
+        const int j = 16 * kb + 4 * g + ii;
+        return j < n_rows && r < br && a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0;
+      });
+    } else if (!pass2) {
+      const int n_left = k_end - n0;
+      if (n_left >= kTileN)
+        attend_block<RB, false>(st, qf, kt, vt, a.scale_log2, [](int, int, int) { return true; });
+      else
+        attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int, int ii, int kb) {
+          return 16 * kb + 4 * g + ii < n_left;
+        });
+      if (imp_raw && wave_imp) {
+        float cs[4];
+        column_sums<RB>(cs, qf, kt, [&](int rb, int ii, float sv) {
+          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? sv : 0.f;
+        });
+        if (g == 0) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        lse_buf[16 * (wr * RB + rb) + l16] =
-            st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
-    }
-    __syncthreads();
-    float lse_r[RB][4];
+          for (int kb = 0; kb < 4; ++kb) imp_buf[s & 1][wr][16 * kb + l16] = cs[kb];
+        }
+      }
+      if (imp_soft && s == n_blk - 1) {
+        // end of the first pass: the rows' log2-sum-exp for the second pass
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+        l_reduced = true;
+        if (g == 0) {
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
-    if (n_blk > 0) {
-      tile_issue<true>(regs[0], csrc, D, blk_n0(blk0), k_end, slot_of);
-      tile_issue<true>(regs[1], csrc, D, blk_n0(blk0 + 1), k_end, slot_of);
-      for (int i = 0; i < per_grp; i += 2) {
+          for (int rb = 0; rb < RB; ++rb)
+            lse_buf[16 * (wr * RB + rb) + l16] =
+                st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
+        }
+      }
+    } else {
+      if (s == n_blk) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int blk = blk0 + i + j;
-          const bool have = i + j < per_grp && blk < blk_end;
-          const int n0 = k_begin + kTileN * blk;
-          __syncthreads();
-          if (have && i + j > 0) flush_imp(n0 - kTileN);
-          if (have) tile_commit<true>(regs[j], lds, tg);
-          tile_issue<true>(regs[j], csrc, D, blk_n0(blk + 2), k_end, slot_of);
-          __syncthreads();
-          if (have && wave_imp) {
-            float cs[4];
-            column_sums<RB>(cs, qf, lds, [&](int rb, int ii, int, float sv) {
-              return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
-                         ? fast_exp2(sv * a.scale_log2 - lse_r[rb][ii])
-                         : 0.f;
-            });
-            if (g == 0) {
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-              for (int kb = 0; kb < 4; ++kb) imp_buf[grp][wr][16 * kb + l16] = cs[kb];
-            }
-          }
+          for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
+      }
+      if (wave_imp) {
+        float cs[4];
+        column_sums<RB>(cs, qf, kt, [&](int rb, int ii, float sv) {
+          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
+                     ? fast_exp2(sv * a.scale_log2 - lse_r[rb][ii])
+                     : 0.f;
+        });
+        if (g == 0) {
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) imp_buf[s & 1][wr][16 * kb + l16] = cs[kb];
         }
       }
     }
-    __syncthreads();
-    if (blk_end > blk0) flush_imp(k_begin + kTileN * (blk_end - 1));
+    barrier_lds_drained();  // step s consumed; step s + 1 landed
+    stage = stage == kStages - 1 ? 0 : stage + 1;
   }
+  if ((imp_raw || imp_soft) && n_steps > 0)
+    flush_imp(n_steps - 1, k_begin + kTileN * (n_blk - 1));
+  if (!l_reduced) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+  }
+  write_out();
 }
 
 // scores[slot] += scale * sum_h imp_part[h][slot] over the keys of each importance tile;
@@ -616,14 +567,11 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
-// Two key groups per workgroup while the grid alone would leave CUs idle.
-constexpr int64_t kSplitBelow = 768;
-
-template <int RB, int NG, bool kVerify>
+template <int RB, bool kVerify>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<RB, NG, kVerify>),
+  hipLaunchKernelGGL((attn_kernel<RB, kVerify>),
                      dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
-                     dim3(kGroupThreads * NG), 0, s, args);
+                     dim3(kThreads), 0, s, args);
   return hipGetLastError();
 }
 
@@ -680,15 +628,8 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool split = n_work * n_heads < kSplitBelow;
-  hipError_t e;
-  // long-row tiles hold two row blocks per wavefront and run one key group (a second group
-  // would not fit the register file)
-  if (tile_rows == 64)
-    e = split ? launch_attn<1, 2, false>(args, n_work, n_heads, s)
-              : launch_attn<1, 1, false>(args, n_work, n_heads, s);
-  else
-    e = launch_attn<2, 1, false>(args, n_work, n_heads, s);
+  const hipError_t e = tile_rows == 64 ? launch_attn<1, false>(args, n_work, n_heads, s)
+                                        : launch_attn<2, false>(args, n_work, n_heads, s);
   FDL_HIP_CHECK(e);
   return ok();
 }
@@ -762,9 +703,7 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   args.d_model = static_cast<int>(d_model);
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = n_vblocks * n_heads < kSplitBelow
-                           ? launch_attn<1, 2, true>(args, n_vblocks, n_heads, s)
-                           : launch_attn<1, 1, true>(args, n_vblocks, n_heads, s);
+  const hipError_t e = launch_attn<1, true>(args, n_vblocks, n_heads, s);
   FDL_HIP_CHECK(e);
   return ok();
 }
