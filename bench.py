@@ -179,6 +179,157 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     return dict(Q=Q, total_ms=total_ms, per_kernel_us=per)
 
 
+def _time_op(fn, reps: int, warm: int = 3) -> float:
+    """Mean microseconds per call of fn() on the current stream (events around the loop)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def run_configs(seed: int = 3, reps: int = 10) -> dict:
+    """Secondary measurements on the other single-layer workloads (bf16, d_model 4096, 32
+    heads): the block-table stress batch (32 sequences, caches of 512-1536 keys in randomly
+    permuted 32-slot pages, a quarter of them full recomputes), its full-recompute tiles on
+    their own, and the Flash-Verify batch (16 sequences, 1024-slot caches, 4-32 candidates
+    each as draft and mask rows). Synthetic N(0,1) activations and N(0,0.02) weights."""
+    import torch
+    from fdl import lib, ops
+    from fdl.generate import verify_mask
+    from fdl.schedule import SeqRows, make_plan
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed)
+    bf = lambda *shape, std=1.0: (torch.randn(shape, generator=gen) * std).to(torch.bfloat16).to(dev)  # noqa: E731
+    scale = 1.0 / np.sqrt(HD)
+    out = {}
+
+    # --- block-table stress
+    NB, P = 32, 32
+    k_ends = rng.integers(512, 1537, NB)
+    full = rng.random(NB) < 0.25
+    pages = [(int(k) + P - 1) // P for k in k_ends]
+    n_pages = int(sum(pages))
+    perm = rng.permutation(n_pages)
+    max_pages = max(pages)
+    table = np.zeros((NB, max_pages), np.int32)
+    nxt = 0
+    for b in range(NB):
+        table[b, :pages[b]] = perm[nxt:nxt + pages[b]]
+        nxt += pages[b]
+    n_slots = n_pages * P
+    seqs, row, slot_list = [], 0, []
+    for b in range(NB):
+        k = int(k_ends[b])
+        logical = np.arange(k) if full[b] else None
+        if logical is None:
+            qn = int(rng.integers(1, 97))
+            m = min(qn, 32)
+            f = int(rng.integers(96, k - 32 + 1))
+            rest = rng.choice(f, qn - m, replace=False) if qn > m else np.zeros(0, np.int64)
+            logical = np.concatenate([np.arange(f, f + m), rest])
+        slot_list.append(table[b, logical // P].astype(np.int64) * P + logical % P)
+        qn = len(logical)
+        seqs.append(SeqRows(batch=b, k_end=k, rows=np.arange(row, row + qn), n_imp=min(qn, 32)))
+        row += qn
+    Q = row
+    slots = torch.from_numpy(np.concatenate(slot_list)).to(dev)
+    x = bf(Q, D)
+    w = [bf(D, D, std=0.02) for _ in range(3)]
+    ang = np.outer(np.arange(1536, dtype=np.float32),
+                   1.0 / (THETA ** (np.arange(0, HD, 2, dtype=np.float32) / HD)))
+    ang = np.concatenate([ang, ang], 1)
+    sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
+    cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
+    rope_row = torch.from_numpy(np.concatenate(
+        [np.arange(len(s)) if full[b] else (s % P) for b, s in enumerate(slot_list)]).astype(np.int64)).to(dev)
+    kc = bf(n_slots, D)
+    vc = bf(n_slots, D)
+    q = torch.empty((Q, D), dtype=torch.bfloat16, device=dev)
+    att = torch.empty_like(q)
+    imp = torch.zeros((H, n_slots), dtype=torch.float32, device=dev)
+    plan = make_plan(seqs, table, 5, device=dev)
+    plan.validate(Q, n_slots)
+    t_qkv = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
+                                                rope_row=rope_row), reps)
+    t_att = _time_op(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
+                                                 lib.IMP_RAW_LOGIT, imp), reps)
+    qk = np.array([len(sq.rows) for sq in seqs], dtype=np.float64)
+    kk = k_ends.astype(np.float64)
+    f_att = float((4.0 * qk * kk * D).sum())
+    b_att = float((2.0 * qk * D * 2 + 2.0 * kk * D * 2).sum())
+    f_qkv = 2.0 * Q * D * 3 * D
+    out["block_table_stress"] = {
+        "workload": f"{NB} sequences, caches 512-1536 keys in permuted 32-slot pages, "
+                    f"{int(full.sum())} full recomputes, {Q} query rows, raw-logit importance",
+        "qkv_rope_cache": {"us": round(t_qkv, 2), "TFLOP/s": round(f_qkv / t_qkv / 1e6, 1),
+                           "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
+        "block_attention": {"us": round(t_att, 2), "TFLOP/s": round(f_att / t_att / 1e6, 1),
+                            "GB/s": round(b_att / t_att / 1e3, 1)},
+    }
+    # full-recompute tiles alone (the MFMA-bound class)
+    fseqs = [sq for sq in seqs if len(sq.rows) == sq.k_end]
+    if fseqs:
+        fplan = make_plan(fseqs, table, 5, device=dev)
+        t_full = _time_op(lambda: ops.block_attention(q, kc, vc, fplan, att, H, scale), reps)
+        ff = float(sum(4.0 * sq.k_end * sq.k_end * D for sq in fseqs))
+        out["block_table_stress"]["full_recompute_attention"] = {
+            "sequences": len(fseqs), "us": round(t_full, 2),
+            "TFLOP/s": round(ff / t_full / 1e6, 1),
+            "mfma_frac": round(ff / t_full / 1e6 / PEAK_BF16_TFLOPS, 4)}
+
+    # --- Flash-Verify
+    NV, LC, BMV = 16, 1024, 32
+    kv = rng.integers(4, 33, NV)
+    rows = 2 * BMV
+    key_pos, vblocks, masks, qslots = [], [], [], []
+    k0 = 0
+    for b in range(NV):
+        S = int(min(kv[b], BMV))
+        cand = b * LC + 512 + np.arange(S)
+        keys = np.setdiff1d(b * LC + np.arange(LC), cand)
+        key_pos.append(keys)
+        vblocks.append([k0, k0 + len(keys), b * rows, b * rows + 2 * S])
+        k0 += len(keys)
+        masks.append(verify_mask(0, S, BMV))
+        qslots.append(np.concatenate([cand, cand, np.full(rows - 2 * S, cand[-1])]))
+    QV = NV * rows
+    xv = bf(QV, D)
+    kcv, vcv = bf(NV * LC, D), bf(NV * LC, D)
+    sinv = torch.from_numpy(np.tile(np.sin(ang[:LC]), (NV, 1)).astype(np.float32)).to(dev)
+    cosv = torch.from_numpy(np.tile(np.cos(ang[:LC]), (NV, 1)).astype(np.float32)).to(dev)
+    qv, k1, v1 = (torch.empty((QV, D), dtype=torch.bfloat16, device=dev) for _ in range(3))
+    attv = torch.empty_like(qv)
+    kp = torch.from_numpy(np.concatenate(key_pos).astype(np.int64)).to(dev)
+    vb = torch.from_numpy(np.array(vblocks, dtype=np.int32)).to(dev)
+    mk = torch.from_numpy(np.concatenate(masks).astype(np.uint8)).to(dev)
+    qs = torch.from_numpy(np.concatenate(qslots).astype(np.int64)).to(dev)
+    t_vq = _time_op(lambda: ops.qkv_rope_cache(xv, *w, sinv, cosv, qs, qv, k1, v1, H,
+                                               kv_packed=True), reps)
+    t_va = _time_op(lambda: ops.verify_attention(qv, k1, v1, kcv, vcv, kp, vb, mk, rows, attv, H,
+                                                 scale), reps)
+    sk = np.minimum(kv, BMV).astype(np.float64)
+    f_va = float((4.0 * (2 * sk) * (LC - sk + 2 * sk) * D).sum())
+    b_va = float((2.0 * (LC - sk) * D * 2 + (LC - sk) * 8 + 2 * (2 * sk) * D * 2).sum())
+    out["flash_verify"] = {
+        "workload": f"{NV} sequences, 1024-slot caches, {int(sk.sum())} candidates as draft "
+                    f"and mask rows ({QV} packed rows incl. padding)",
+        "qkv_rope_cache_packed": {"us": round(t_vq, 2)},
+        "verify_attention": {"us": round(t_va, 2), "GB/s": round(b_va / t_va / 1e3, 1),
+                             "hbm_frac": round(b_va / t_va / 1e3 / PEAK_HBM_GBS, 4),
+                             "TFLOP/s": round(f_va / t_va / 1e6, 1)},
+    }
+    return out
+
+
 def run_cpu_baseline(budget_s: float = 15.0, seed: int = 2) -> dict:
     """Times the numpy oracle (one layer of the same workload) on the host cores."""
     from oracle import flash_cache_oracle as orc
@@ -284,6 +435,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-e2e", action="store_true", help="skip the LLaDA-8B decode leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the block-table stress and Flash-Verify measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run five 100 MiB device-to-device copies (the reference kernel for "
                          "scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -350,6 +503,8 @@ def main() -> int:
                      "traffic_source": TRAFFIC_FILE.name},
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
+    if not args.no_configs:
+        out["configs"] = run_configs()
     if not args.no_e2e:
         out["e2e_llada8b"] = run_e2e(args.e2e_steps, args.e2e_torch_steps)
     if not args.no_cpu:

@@ -152,13 +152,16 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) sc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int sd = 0; sd < 4; ++sd) {
       const bf16x8 kf = k_frag(kt, kb, sd, l16, g);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) sc[rb][kb] = mfma16(kf, qf[rb][sd], sc[rb][kb]);
     }
+    // with two row blocks, keep the fragment reads of one 16-key block in flight at a time
+    if constexpr (RB > 1) __builtin_amdgcn_sched_barrier(0);
+  }
   bf16x8 pb[RB][2];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -198,13 +201,15 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
       }
   }
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+  for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const bf16x8 vf = vt_frag(vt, ks, db, l16, g);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma16(vf, pb[rb][ks], st.o[rb][db]);
     }
+    if constexpr (RB > 1) __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // Column sums over the wave's importance rows of S = Q K^T for the 64 keys of a block:
@@ -245,6 +250,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   __shared__ float imp_buf[2][4][kTileN];   // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
+  __shared__ float qsum_buf[kHeadDim];        // raw importance: sum of the importance rows' Q
+  __shared__ u32x4 qsum_frag_buf[4][64];      // its MFMA A-operand fragments, by lane
 
   const int tid = threadIdx.x;
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
@@ -436,8 +443,38 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
     }
   };
 
-  barrier_only();  // #0
-  barrier_only();  // #1: step 0 landed
+  // Raw importance is linear in Q: the column sums over the importance rows of Q K^T are
+  // (sum of those rows' Q) K^T. The fp32 sum is split into bf16 hi + lo parts, rows 0 and 1
+  // of one 16-row MFMA operand, so one wavefront per block computes all 64 sums.
+  if (imp_raw && tid < kHeadDim) {
+    float acc = 0.f;
+    for (int r = 0; r < n_imp; ++r) {
+      const int64_t qr = int64_t(a.row_idx[roff + r]);
+      if (qr >= 0 && qr < a.n_q_rows) acc += bf2f(a.q[qr * D + col0 + tid]);
+    }
+    qsum_buf[tid] = acc;
+  }
+  barrier_lds_drained();  // #0
+  // A-operand fragment sd of the summed Q: row 0 (lane l16 == 0) the bf16 part, row 1 the
+  // remainder, other rows zero; built once by wave sd.
+  if (imp_raw) {
+    u32x4 w = {0, 0, 0, 0};
+    if (l16 < 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = qsum_buf[32 * wr + 8 * g + 2 * j + e];
+          const float hi = bf2f(f2bf(x));
+          v[e] = l16 == 0 ? hi : x - hi;
+        }
+        w[j] = pack_bf16x2(v[0], v[1]);
+      }
+    }
+    qsum_frag_buf[wr][lane] = w;
+  }
+  barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
   int stage = 0;
   for (int s = 0; s < n_steps; ++s) {
@@ -447,8 +484,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
     const bool in_blk = kVerify && inblock && s == n_steps - 1;
     const int blk = pass2 ? s - n_blk : s;
     const int n0 = k_begin + kTileN * blk;
-    if ((imp_raw || imp_soft) && s > 0 && (s - 1 < n_blk ? imp_raw : true))
-      flush_imp(s - 1, k_begin + kTileN * ((s - 1) >= n_blk ? s - 1 - n_blk : s - 1));
+    if (imp_soft && s > n_blk) flush_imp(s - 1, k_begin + kTileN * (s - 1 - n_blk));
     if (in_blk) {
       const int br = a.block_rows;
       attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int rb, int ii, int kb) {
@@ -458,21 +494,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
       });
     } else if (!pass2) {
       const int n_left = k_end - n0;
-      if (n_left >= kTileN)
+      // The unmasked variant of full blocks saves the per-logit key test; with two row
+      // blocks per wavefront a second inlined copy of the block would not fit the registers.
+      if (RB == 1 && n_left >= kTileN)
         attend_block<RB, false>(st, qf, kt, vt, a.scale_log2, [](int, int, int) { return true; });
       else
         attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int, int ii, int kb) {
           return 16 * kb + 4 * g + ii < n_left;
         });
-      if (imp_raw && wave_imp) {
-        float cs[4];
-        column_sums<RB>(cs, qf, kt, [&](int rb, int ii, float sv) {
-          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp ? sv : 0.f;
-        });
-        if (g == 0) {
+      if (imp_raw) {
+        // wave wr: the 16 keys of key block kb = wr
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) imp_buf[s & 1][wr][16 * kb + l16] = cs[kb];
-        }
+        for (int sd = 0; sd < 4; ++sd)
+          acc = mfma16(as_bf16x8(qsum_frag_buf[sd][lane]), k_frag(kt, wr, sd, l16, g), acc);
+        const int n = n0 + 16 * wr + l16;
+        if (g == 0 && n < k_end) imp_out[slot_of(n)] = acc[0] + acc[1];  // rows hi + lo
       }
       if (imp_soft && s == n_blk - 1) {
         // end of the first pass: the rows' log2-sum-exp for the second pass
@@ -509,8 +546,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
     barrier_lds_drained();  // step s consumed; step s + 1 landed
     stage = stage == kStages - 1 ? 0 : stage + 1;
   }
-  if ((imp_raw || imp_soft) && n_steps > 0)
-    flush_imp(n_steps - 1, k_begin + kTileN * (n_blk - 1));
+  if (imp_soft && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * (n_blk - 1));
   if (!l_reduced) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
