@@ -71,6 +71,20 @@ __device__ __forceinline__ int xcd_tile(int bid, int n_tiles) {
   return (n_tiles & 7) == 0 ? (bid & 7) * (n_tiles >> 3) + (bid >> 3) : bid;
 }
 
+// Tile t -> (n-block, m-block). Tiles come in groups of kGroupM m-blocks: within a group
+// the m-block varies fastest, so the tiles running at the same time on one XCD share both
+// X row blocks (kGroupM of them) and weight slices (one per kGroupM tiles) in its L2.
+// With at most kGroupM m-blocks this is the plain n-block-major order.
+constexpr int kGroupM = 8;
+__device__ __forceinline__ void tile_coords(int t, int n_mtiles, int n_tiles, int& nt, int& mt) {
+  const int n_ntiles = n_tiles / n_mtiles;
+  const int per_group = kGroupM * n_ntiles;
+  const int grp = t / per_group, r = t - grp * per_group;
+  const int gm = min(kGroupM, n_mtiles - grp * kGroupM);  // m-blocks in this group
+  nt = r / gm;
+  mt = grp * kGroupM + (r - nt * gm);
+}
+
 // Destination rows of tile rows m0 .. m0 + BM - 1, written by threads 0 .. BM - 1:
 // dst[0] = Q row, dst[1] = K/V row (cache slot, or the packed row), rope = sin/cos row.
 // A row past n_rows, or with an out-of-range slot or rope row, gets -1 (skipped in all
@@ -134,9 +148,8 @@ __global__ __launch_bounds__(kThreads, OCC) void qkv_stream_kernel(QkvArgs a) {
   __shared__ int64_t s_rope[BM];
 
   const int tid = threadIdx.x;
-  const int t = xcd_tile(blockIdx.x, a.n_tiles);
-  const int nt = t / a.n_mtiles;
-  const int mt = t - nt * a.n_mtiles;
+  int nt, mt;
+  tile_coords(xcd_tile(blockIdx.x, a.n_tiles), a.n_mtiles, a.n_tiles, nt, mt);
   const int64_t m0 = int64_t(mt) * BM;
   const int D = a.d_model;
   const int pairs_per_mat = a.n_heads * kHalf;
@@ -322,9 +335,8 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
   __shared__ int64_t s_rope[kPcBM];
 
   const int tid = threadIdx.x;
-  const int t = xcd_tile(blockIdx.x, a.n_tiles);
-  const int nt = t / a.n_mtiles;
-  const int mt = t - nt * a.n_mtiles;
+  int nt, mt;
+  tile_coords(xcd_tile(blockIdx.x, a.n_tiles), a.n_mtiles, a.n_tiles, nt, mt);
   const int64_t m0 = int64_t(mt) * kPcBM;
   const int D = a.d_model;
   const int pairs_per_mat = a.n_heads * kHalf;
