@@ -138,12 +138,19 @@ __device__ __forceinline__ bf16x8 vt_frag(const uint8_t* vt, int ks, int db, int
   return as_bf16x8(w);
 }
 
-// One 64-key block of online softmax + PV for the wave's RB row blocks. valid(rb, i, kb):
-// may row block rb's lane row attend key 16*kb + 4*(l/16) + i of the block?
-template <int RB, bool kMasked, typename Valid>
+// Running maxima are raised lazily: a row keeps its reference maximum until a block's
+// logits exceed it by more than kLazyMax (log2 domain, a factor of 256), so the rescale of
+// O and l is skipped for most blocks. Probabilities then stay below 256 (fp32 and bf16
+// represent them to the same relative precision) and O / l is unchanged.
+constexpr float kLazyMax = 8.f;
+
+// One 64-key block of online softmax + PV for the wave's RB row blocks. bias(rb, kb, i) is
+// 0 when row block rb's lane row may attend key 16*kb + 4*(l/16) + i of the block and
+// -infinity when it may not.
+template <int RB, typename Bias>
 __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf)[RB][4],
                                              const u32x4* kt, const uint8_t* vt,
-                                             float scale_log2, Valid valid) {
+                                             float scale_log2, Bias bias) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
   f32x4 sc[RB][4];
@@ -162,7 +169,8 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
     // with two row blocks, keep the fragment reads of one 16-key block in flight at a time
     if constexpr (RB > 1) __builtin_amdgcn_sched_barrier(0);
   }
-  bf16x8 pb[RB][2];
+  float alpha[RB];
+  bool rescale = false;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     float tmax = -INFINITY;
@@ -170,15 +178,16 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = sc[rb][kb][i] * scale_log2;
-        if constexpr (kMasked) v = valid(rb, i, kb) ? v : -INFINITY;
+        const float v = __builtin_fmaf(sc[rb][kb][i], scale_log2, bias(rb, kb, i));
         sc[rb][kb][i] = v;
         tmax = fmaxf(tmax, v);
       }
     tmax = xmax(tmax);
-    const float m_new = fmaxf(st.m[rb], tmax);
+    const bool raise = tmax > st.m[rb] + kLazyMax;
+    const float m_new = raise ? tmax : st.m[rb];
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // nothing attended yet
-    const float alpha = fast_exp2(st.m[rb] - m_use);
+    alpha[rb] = raise ? fast_exp2(st.m[rb] - m_use) : 1.f;
+    rescale = rescale || raise;
     st.m[rb] = m_new;
     float psum = 0.f;
 #pragma unroll
@@ -189,9 +198,18 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
         sc[rb][kb][i] = p;
         psum += p;
       }
-    st.l[rb] = st.l[rb] * alpha + psum;
+    st.l[rb] = st.l[rb] * alpha[rb] + psum;
+  }
+  if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
 #pragma unroll
-    for (int db = 0; db < 8; ++db) st.o[rb][db] *= alpha;
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int db = 0; db < 8; ++db) st.o[rb][db] *= alpha[rb];
+  }
+  // k-slot (g, j) of PV step ks is key 32ks + 4g + j (j < 4) or 32ks + 16 + 4g + (j - 4)
+  bf16x8 pb[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -199,7 +217,6 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
         pb[rb][ks][j] = static_cast<__bf16>(sc[rb][2 * ks][j]);
         pb[rb][ks][j + 4] = static_cast<__bf16>(sc[rb][2 * ks + 1][j]);
       }
-  }
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -487,21 +504,24 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
     if (imp_soft && s > n_blk) flush_imp(s - 1, k_begin + kTileN * (s - 1 - n_blk));
     if (in_blk) {
       const int br = a.block_rows;
-      attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int rb, int ii, int kb) {
+      attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
         const int r = 16 * (wr * RB + rb) + l16;
         const int j = 16 * kb + 4 * g + ii;
-        return j < n_rows && r < br && a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0;
+        return j < n_rows && r < br && a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0
+                   ? 0.f
+                   : -INFINITY;
       });
     } else if (!pass2) {
+      // keys past k_end (the tail of the last block) get a -infinity bias
       const int n_left = k_end - n0;
-      // The unmasked variant of full blocks saves the per-logit key test; with two row
-      // blocks per wavefront a second inlined copy of the block would not fit the registers.
-      if (RB == 1 && n_left >= kTileN)
-        attend_block<RB, false>(st, qf, kt, vt, a.scale_log2, [](int, int, int) { return true; });
-      else
-        attend_block<RB, true>(st, qf, kt, vt, a.scale_log2, [&](int, int ii, int kb) {
-          return 16 * kb + 4 * g + ii < n_left;
-        });
+      float kbias[4][4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          kbias[kb][ii] = 16 * kb + 4 * g + ii < n_left ? 0.f : -INFINITY;
+      attend_block<RB>(st, qf, kt, vt, a.scale_log2,
+                       [&](int, int kb, int ii) { return kbias[kb][ii]; });
       if (imp_raw) {
         // wave wr: the 16 keys of key block kb = wr
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
