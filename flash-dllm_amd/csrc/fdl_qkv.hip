@@ -16,11 +16,12 @@
 //
 // Two kernels, chosen by the number of rows:
 //  * qkv_pc_kernel (more than 64 rows): 128 rows x 96 pairs per workgroup (512 rows: one
-//    tile per CU). Eight wavefronts in two roles: four producers move the X and W tiles of
-//    each 64-wide reduction step straight from global memory into LDS (global_load_lds,
-//    three LDS stages in flight), and four consumers run the 16x16x32 MFMAs from LDS. A
-//    consumer never issues a global memory instruction, so it is never held behind the
-//    texture-address queue while its SIMD's MFMA unit waits; a producer shares that SIMD.
+//    tile per CU). Sixteen wavefronts in two roles: four producers move the X and W tiles
+//    of each 64-wide reduction step straight from global memory into LDS (global_load_lds,
+//    three LDS stages in flight), and twelve consumers (three per SIMD) run the 16x16x32
+//    MFMAs from LDS. A consumer never issues a global memory instruction, so it is never
+//    held behind the texture-address queue, and the three consumers of a SIMD hide each
+//    other's LDS latency.
 //  * qkv_stream_kernel<BM, BP> (up to 64 rows, weight streaming): 64 rows x 32 pairs per
 //    workgroup so the launch covers the CUs; X and W tiles staged through LDS with the
 //    global loads kStages steps ahead in a ring of registers and the LDS fragment reads of
@@ -304,11 +305,11 @@ __global__ __launch_bounds__(kThreads, OCC) void qkv_stream_kernel(QkvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// qkv_pc_kernel: 128 rows x 96 pairs; consumer wavefront (wm, wn) owns rows 64 wm .. + 64
-// and pairs 48 wn .. + 48 (low and high columns).
+// qkv_pc_kernel: 128 rows x 96 pairs; consumer wavefront (wm, wn), wm < 4, wn < 3, owns rows
+// 32 wm .. + 32 and pairs 32 wn .. + 32 (low and high columns).
 constexpr int kPcBM = 128;
 constexpr int kPcBP = 96;
-constexpr int kPcThreads = 512;
+constexpr int kPcThreads = 1024;  // 12 consumer + 4 producer wavefronts
 constexpr int kPcStages = 3;                         // LDS stages
 constexpr int kPcABytes = kPcBM * 128;               // X tile of one step (16 KB)
 constexpr int kPcStageBytes = kPcABytes + 2 * kPcBP * 128;  // + W tile (24 KB)
@@ -329,7 +330,7 @@ __device__ __forceinline__ void barrier_lds_drained() {
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
 __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
-  constexpr int kWP = kPcBP / 2, kPB = kWP / 16;
+  constexpr int kWP = kPcBP / 3, kPB = kWP / 16;
   __shared__ __align__(1024) uint8_t smem[kPcStages * kPcStageBytes];
   __shared__ int64_t s_dst[2][kPcBM];
   __shared__ int64_t s_rope[kPcBM];
@@ -344,8 +345,8 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
   // wavefront executes only its own role's barriers (both roles execute 1 + nk of them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const bool producer = wave >= 4;
-  const int pw = wave & 3;
+  const bool producer = wave >= 12;
+  const int pw = wave - 12;
   const int nk = D / kKT;
 
   if (producer) {
@@ -396,11 +397,11 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
     return;
   }
 
-  const int wm = pw >> 1, wn = pw & 1;
+  const int wm = wave / 3, wn = wave - 3 * (wave / 3);  // rows 32 wm .., pairs 32 wn ..
   const int l16 = lane & 15, g4 = lane >> 4;
   const int sw = (l16 >> 1) & 7;
   struct Frag {
-    u32x4 a[4];
+    u32x4 a[2];
     u32x4 b[2][kPB];
   };
   // MFMA operands of half-step ss of the step in `stage`: lane (l16, g4) takes logical chunk
@@ -409,23 +410,23 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
     const u32x4* st = reinterpret_cast<const u32x4*>(smem + stage * kPcStageBytes);
     const int c = (4 * ss + g4) ^ sw;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) f.a[rb] = st[(64 * wm + 16 * rb + l16) * 8 + c];
+    for (int rb = 0; rb < 2; ++rb) f.a[rb] = st[(32 * wm + 16 * rb + l16) * 8 + c];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int pb = 0; pb < kPB; ++pb)
         f.b[h][pb] = st[kPcABytes / 16 + (kPcBP * h + kWP * wn + 16 * pb + l16) * 8 + c];
   };
-  f32x4 acc[4][2][kPB];
+  f32x4 acc[2][2][kPB];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mma = [&](const Frag& f) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -435,11 +436,11 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
   // one LDS read between two MFMAs
   auto interleave = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4 + 2 * kPB; ++i) {
+    for (int i = 0; i < 2 + 2 * kPB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8 * kPB - 2 * (4 + 2 * kPB), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * kPB - (2 + 2 * kPB), 0);
   };
 
   Frag f0, f1;
@@ -461,17 +462,17 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
     stage = next;
   }
 
-  // Epilogue: acc[rb][h][pb][i] is row 64 wm + 16 rb + 4 g4 + i, pair
-  // 96 nt + 48 wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
+  // Epilogue: acc[rb][h][pb][i] is row 32 wm + 16 rb + 4 g4 + i, pair
+  // 96 nt + 32 wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
 #pragma unroll
   for (int pb = 0; pb < kPB; ++pb) {
     const int p = kPcBP * nt + kWP * wn + 16 * pb + l16;
     const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 64 * wm + 16 * rb + 4 * g4 + i;
+        const int row = 32 * wm + 16 * rb + 4 * g4 + i;
         const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
         if (dst < 0) continue;
         store_pair(a, mat, dst, s_rope[row], rem >> 6, rem & 63, acc[rb][0][pb][i],
