@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kTileN = 64;                    // keys per block
-constexpr int kThreads = 512;                 // 4 consumer + 4 producer wavefronts
+constexpr int kProducers = 4;                 // producer wavefronts per workgroup
 constexpr int kStages = 4;                    // LDS blocks in flight
 constexpr int kTileBytes = kTileN * 256;      // one K (or V) block: 16 KB
 constexpr int kStageBytes = 2 * kTileBytes;   // K then V
@@ -260,11 +260,11 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
 //   [0, n_blk)          cache blocks, K and V
 //   [n_blk, 2 n_blk)    softmax importance only: the cache blocks again, K only
 //   n_blk               verify only (when the block has rows): the in-block keys
-template <int RB, bool kVerify>
-__global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
-  constexpr int kRows = 64 * RB;
+template <int RB, int NC, bool kVerify>
+__global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
+  constexpr int kRows = 16 * RB * NC;
   __shared__ __align__(1024) uint8_t smem[kStages * kStageBytes];
-  __shared__ float imp_buf[2][4][kTileN];   // per-wave column sums of a block, by parity
+  __shared__ float imp_buf[2][NC][kTileN];  // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
   __shared__ float qsum_buf[kHeadDim];        // raw importance: sum of the importance rows' Q
@@ -274,8 +274,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
   // wavefront executes only its own role's barriers (both roles execute 2 + n_steps).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const bool producer = wave >= 4;
-  const int wr = wave & 3;
+  const bool producer = wave >= NC;
+  const int wr = producer ? wave - NC : wave;  // producer index or consumer index
   const int l16 = lane & 15, g = lane >> 4;
   const int h = blockIdx.y;
   const int64_t D = a.d_model;
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   };
 
   if (producer) {
-    const int tp = tid - 256;
+    const int tp = tid - 64 * NC;
     if (slots_staged) {
       for (int i = tp; i < k_end - k_begin; i += 256)
         slot_buf[i] = static_cast<int32_t>(lookup(k_begin + i));
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   // wave sums 16 keys over the waves' partials. Runs after the barrier that follows the
   // partials' writes and before the barrier after which they are overwritten.
   auto flush_imp = [&](int s, int n0) {
-    if (l16 == lane) {  // lanes 0..15
+    if (wr < 4 && l16 == lane) {  // lanes 0..15 of the first four consumers
       const int key = 16 * wr + lane;
       const int n = n0 + key;
       if (n < k_end) {
@@ -474,7 +474,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
   barrier_lds_drained();  // #0
   // A-operand fragment sd of the summed Q: row 0 (lane l16 == 0) the bf16 part, row 1 the
   // remainder, other rows zero; built once by wave sd.
-  if (imp_raw) {
+  if (imp_raw && wr < 4) {
     u32x4 w = {0, 0, 0, 0};
     if (l16 < 2) {
 #pragma unroll
@@ -522,8 +522,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnArgs a) {
           kbias[kb][ii] = 16 * kb + 4 * g + ii < n_left ? 0.f : -INFINITY;
       attend_block<RB>(st, qf, kt, vt, a.scale_log2,
                        [&](int, int kb, int ii) { return kbias[kb][ii]; });
-      if (imp_raw) {
-        // wave wr: the 16 keys of key block kb = wr
+      if (imp_raw && wr < 4) {
+        // consumer wr < 4: the 16 keys of key block kb = wr
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sd = 0; sd < 4; ++sd)
@@ -623,11 +623,11 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
-template <int RB, bool kVerify>
+template <int RB, int NC, bool kVerify>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<RB, kVerify>),
+  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>),
                      dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
-                     dim3(kThreads), 0, s, args);
+                     dim3(64 * (NC + kProducers)), 0, s, args);
   return hipGetLastError();
 }
 
@@ -684,8 +684,9 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = tile_rows == 64 ? launch_attn<1, false>(args, n_work, n_heads, s)
-                                        : launch_attn<2, false>(args, n_work, n_heads, s);
+  // 64-row tiles: four consumers of 16 rows; 128-row tiles: eight consumers (two per SIMD)
+  const hipError_t e = tile_rows == 64 ? launch_attn<1, 4, false>(args, n_work, n_heads, s)
+                                        : launch_attn<1, 8, false>(args, n_work, n_heads, s);
   FDL_HIP_CHECK(e);
   return ok();
 }
@@ -759,7 +760,7 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   args.d_model = static_cast<int>(d_model);
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = launch_attn<1, true>(args, n_vblocks, n_heads, s);
+  const hipError_t e = launch_attn<1, 4, true>(args, n_vblocks, n_heads, s);
   FDL_HIP_CHECK(e);
   return ok();
 }
