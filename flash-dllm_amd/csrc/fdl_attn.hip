@@ -32,6 +32,8 @@
 #include "fdl_device.h"
 #include "fdl_host.h"
 
+#include <type_traits>
+
 namespace fdl {
 namespace {
 
@@ -78,6 +80,7 @@ struct AttnArgs {
   int tile_rows;
   int imp_mode;
   float scale_log2;  // softmax_scale * log2(e)
+  int split;         // 1: workgroup 2i + j runs rows [128 j, 128 j + 128) of 256-row item i
 };
 
 template <int RB>
@@ -87,13 +90,26 @@ struct RowState {
   f32x4 o[RB][8];   // O^T blocks: lane holds O[row][16*db + 4*(l/16) + i]
 };
 
+// Reductions over the four 16-lane rows of a wavefront (lane ^ 16, lane ^ 32) with gfx950's
+// row-swap permutes, which run on the VALU and add no LDS traffic: permlane16_swap(x, x)
+// returns {x of rows (0, 0, 2, 2), x of rows (1, 1, 3, 3)}, permlane32_swap(x, x) returns
+// {rows (0, 1, 0, 1), rows (2, 3, 2, 3)}. The association matches a butterfly over xor 16
+// then xor 32, so every lane gets the same bits.
 __device__ __forceinline__ float xmax(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+  const auto a =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float xsum(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+  const auto a =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Waits until at most n global loads of this wavefront are outstanding (n a multiple of
@@ -293,13 +309,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     if (row0 < 0 || int64_t(row0) + n_rows > a.n_q_rows) n_rows = 0;
     if (n_rows > a.block_rows) n_rows = a.block_rows;  // mask rows hold block_rows columns
   } else {
-    const int32_t* it = a.work + 8 * blockIdx.x;
+    const int half = a.split ? int(blockIdx.x & 1) : 0;
+    const int32_t* it = a.work + 8 * (a.split ? blockIdx.x >> 1 : blockIdx.x);
     b = it[0];
     k_begin = it[1];
     k_end = it[2];
-    roff = it[3];
-    n_rows = it[4];
-    n_imp = a.imp_mode ? it[5] : 0;
+    roff = it[3] + 128 * half;
+    n_rows = it[4] - 128 * half;
+    n_imp = a.imp_mode && half == 0 ? it[5] : 0;
     if (b < 0 || b >= a.n_seq || k_begin < 0 ||
         int64_t(k_end) > (int64_t(a.max_pages) << a.page_log2)) {
       b = 0;
@@ -309,6 +326,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   }
   if (n_rows > kRows) n_rows = kRows;
   if (n_rows < 0) n_rows = 0;
+  if (!kVerify && n_rows == 0) return;  // the empty upper half of a split 128-row item
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
 
@@ -574,6 +592,438 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   write_out();
 }
 
+// ------------------------------------------------------------------------------------------
+// Long tiles (up to 256 query rows of one sequence x one head), for full recomputes.
+//
+// Eight wavefronts of 32 rows each in two groups, A (waves 0-3) and B (waves 4-7), one of
+// each per SIMD. Every 64-key block j goes through an MFMA phase M_j (PV of block j-1, QK of
+// block j) and a softmax phase V_j; group B runs one half-step behind group A, so in every
+// half-step each SIMD has one wavefront issuing MFMAs and one running the softmax:
+//   half-step 2j:     A: M_j                        B: V_{j-1}
+//   half-step 2j + 1: A: V_j + transpose of V_j    B: M_j
+// with a workgroup barrier between half-steps. Group A also moves the blocks: it issues the
+// global -> LDS loads of block j + 2 at the start of M_j into a three-deep ring (K and
+// row-major V of a block, 32 KB) and rewrites each V block, after its softmax, into a
+// fragment-major V^T buffer (two, by block parity) from which both groups read the
+// O^T = V^T P^T operands with one 16-byte read per lane instead of two transposing reads.
+//
+// The loads are issued from inline assembly: the compiler then does not know them and
+// inserts no wait for them before unrelated LDS reads; the waves wait for their own loads
+// explicitly (s_waitcnt vmcnt) before the barrier that hands a block to the readers.
+constexpr int kLongRows = 256;
+constexpr int kLongStages = 3;
+constexpr int kLongLoads = 8;  // 1 KB loads per group-A wavefront per block (4 K + 4 V)
+
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane (lds wavefront-uniform).
+// M0 carries the LDS address; its previous value is restored.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds)
+      : "memory");
+}
+
+// Waits until at most n of this wavefront's global loads are outstanding (n = 0, 8, 16).
+__device__ __forceinline__ void wait_loads(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+  }
+}
+
+struct LongState {
+  float m[2];
+  float l[2];
+  f32x4 o[2][8];
+};
+
+// V^T fragment i = 8 ks + db of the fragment-major buffer: one 16-byte read per lane.
+__device__ __forceinline__ bf16x8 vtf_frag(const u32x4* vtf, int i, int lane) {
+  return as_bf16x8(vtf[i * 64 + lane]);
+}
+
+// Rewrites fragments 4 wq .. 4 wq + 3 of a row-major V block as fragment-major V^T.
+__device__ __forceinline__ void transpose_v(const uint8_t* vrow, u32x4* vtf, int wq, int lane) {
+  const int l16 = lane & 15, g = lane >> 4;
+  bf16x8 f[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * wq + j;
+    f[j] = vt_frag(vrow, i >> 3, i & 7, l16, g);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vtf[(4 * wq + j) * 64 + lane] = __builtin_bit_cast(u32x4, f[j]);
+}
+
+__device__ __forceinline__ void long_qk(f32x4 (&sc)[2][4], const bf16x8 (&qf)[2][4],
+                                        const u32x4* kt, int l16, int g) {
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int sd = 0; sd < 4; ++sd) {
+      const bf16x8 kf = k_frag(kt, kb, sd, l16, g);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) sc[rb][kb] = mfma16(kf, qf[rb][sd], sc[rb][kb]);
+    }
+}
+
+__device__ __forceinline__ void long_pv(LongState& st, const bf16x8 (&pb)[2][2], const u32x4* vtf,
+                                        int lane) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const bf16x8 vf = vtf_frag(vtf, i, lane);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) st.o[rb][i & 7] = mfma16(vf, pb[rb][i >> 3], st.o[rb][i & 7]);
+  }
+}
+
+// M phase: PV of the previous block and QK of the current one in one schedule, the fragment
+// reads three fragments ahead of the MFMAs that consume them. QK fragments go sd-major so
+// consecutive MFMAs accumulate into different tiles.
+__device__ __forceinline__ void long_pv_qk(LongState& st, const bf16x8 (&pb)[2][2],
+                                           const u32x4* vtf, f32x4 (&sc)[2][4],
+                                           const bf16x8 (&qf)[2][4], const u32x4* kt, int lane) {
+  const int l16 = lane & 15, g = lane >> 4;
+  bf16x8 vf[16], kf[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) vf[i] = vtf_frag(vtf, i, lane);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kf[i] = k_frag(kt, i & 3, i >> 2, l16, g);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) st.o[rb][i & 7] = mfma16(vf[i], pb[rb][i >> 3], st.o[rb][i & 7]);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) sc[rb][i & 3] = mfma16(kf[i], qf[rb][i >> 2], sc[rb][i & 3]);
+  __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // DS reads
+#pragma unroll
+  for (int i = 0; i < 29; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+}
+
+// V phase: online softmax of one block's logits (lane rows l % 16 of both row blocks), the
+// lazily raised running maximum and the bf16 probabilities as PV operands. With kTail, keys
+// 16 kb + 4 (l / 16) + i >= n_left are masked.
+template <bool kTail>
+__device__ __forceinline__ void long_softmax(LongState& st, f32x4 (&sc)[2][4], bf16x8 (&pb)[2][2],
+                                             float scale_log2, int n_left, int g) {
+  float alpha[2];
+  bool rescale = false;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float bias = 0.f;
+        if constexpr (kTail) bias = 16 * kb + 4 * g + i < n_left ? 0.f : -INFINITY;
+        const float v = __builtin_fmaf(sc[rb][kb][i], scale_log2, bias);
+        sc[rb][kb][i] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = xmax(tmax);
+    const bool raise = tmax > st.m[rb] + kLazyMax;
+    const float m_new = raise ? tmax : st.m[rb];
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    alpha[rb] = raise ? fast_exp2(st.m[rb] - m_use) : 1.f;
+    rescale = rescale || raise;
+    st.m[rb] = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(sc[rb][kb][i] - m_use);
+        sc[rb][kb][i] = p;
+        psum += p;
+      }
+    st.l[rb] = st.l[rb] * alpha[rb] + psum;
+  }
+  if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int db = 0; db < 8; ++db) st.o[rb][db] *= alpha[rb];
+  }
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pb[rb][ks][j] = static_cast<__bf16>(sc[rb][2 * ks][j]);
+        pb[rb][ks][j + 4] = static_cast<__bf16>(sc[rb][2 * ks + 1][j]);
+      }
+}
+
+// Importance: none or raw logits (the softmax-colsum mode runs the 128-row kernel on split
+// items). Both groups execute 3 + 2 n_blk barriers.
+__global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
+  __shared__ __align__(1024) uint8_t smem[kLongStages * kStageBytes];
+  __shared__ __align__(1024) u32x4 vtb[2][kTileBytes / 16];  // fragment-major V^T by parity
+  __shared__ int32_t slot_buf[kSlotCache];
+  __shared__ float qsum_buf[kHeadDim];
+  __shared__ u32x4 qsum_frag_buf[4][64];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const bool grp_a = wave < 4;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y;
+  const int64_t D = a.d_model;
+  const int col0 = h * kHeadDim;
+
+  const int32_t* it = a.work + 8 * blockIdx.x;
+  int b = it[0], k_begin = it[1], k_end = it[2], roff = it[3], n_rows = it[4];
+  int n_imp = a.imp_mode ? it[5] : 0;
+  if (b < 0 || b >= a.n_seq || k_begin < 0 ||
+      int64_t(k_end) > (int64_t(a.max_pages) << a.page_log2)) {
+    b = 0;
+    k_end = k_begin;
+  }
+  if (roff < 0 || int64_t(roff) + (n_rows > 0 ? n_rows : 0) > a.n_row_idx) n_rows = 0;
+  if (n_rows > kLongRows) n_rows = kLongRows;
+  if (n_rows < 0) n_rows = 0;
+  if (n_imp > n_rows) n_imp = n_rows;
+  if (k_end < k_begin) k_end = k_begin;
+  const bool imp_raw = n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
+  const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
+
+  const int pl = a.page_log2;
+  const int pmask = (1 << pl) - 1;
+  const int32_t* ptab = a.page_table + int64_t(b) * a.max_pages;
+  const int64_t n_slots = a.n_slots;
+  auto lookup = [&](int n) -> int64_t {
+    const int64_t s = (int64_t(ptab[n >> pl]) << pl) | (n & pmask);
+    return (s >= 0 && s < n_slots) ? s : 0;  // the host validators reject such tables
+  };
+  const bool slots_staged = k_end - k_begin <= kSlotCache && n_slots < (int64_t(1) << 31);
+  auto slot_of = [&](int n) -> int64_t {
+    return slots_staged ? int64_t(slot_buf[n - k_begin]) : lookup(n);
+  };
+  if (slots_staged) {
+    for (int i = tid; i < k_end - k_begin; i += 64 * 8)
+      slot_buf[i] = static_cast<int32_t>(lookup(k_begin + i));
+  }
+
+  // the wave's query rows: 32 wave + 16 rb + (lane % 16)
+  int64_t qrow[2];
+  bf16x8 qf[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int r = 32 * wave + 16 * rb + l16;
+    qrow[rb] = -1;
+    if (r < n_rows) {
+      const int64_t q = int64_t(a.row_idx[roff + r]);
+      if (q >= 0 && q < a.n_q_rows) qrow[rb] = q;
+    }
+#pragma unroll
+    for (int sd = 0; sd < 4; ++sd) {
+      u32x4 v = {0, 0, 0, 0};
+      if (qrow[rb] >= 0) v = ld16(a.q + qrow[rb] * D + col0 + 32 * sd + 8 * g);
+      qf[rb][sd] = as_bf16x8(v);
+    }
+  }
+  if (imp_raw && tid < kHeadDim) {
+    float acc = 0.f;
+    for (int r = 0; r < n_imp; ++r) {
+      const int64_t qr = int64_t(a.row_idx[roff + r]);
+      if (qr >= 0 && qr < a.n_q_rows) acc += bf2f(a.q[qr * D + col0 + tid]);
+    }
+    qsum_buf[tid] = acc;
+  }
+  __syncthreads();
+  // raw importance: summed Q as bf16 hi + lo rows of one MFMA operand (see attn_kernel)
+  if (imp_raw && wave < 4) {
+    u32x4 w = {0, 0, 0, 0};
+    if (l16 < 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = qsum_buf[32 * wave + 8 * g + 2 * j + e];
+          const float hi = bf2f(f2bf(x));
+          v[e] = l16 == 0 ? hi : x - hi;
+        }
+        w[j] = pack_bf16x2(v[0], v[1]);
+      }
+    }
+    qsum_frag_buf[wave][lane] = w;
+  }
+  // The Q loads are waited for here, before the first block load is issued: a later wait
+  // the compiler places for them would also wait for every block load issued since.
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int sd = 0; sd < 4; ++sd) asm volatile("" ::"v"(qf[rb][sd]));
+  __syncthreads();
+
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_ptr)smem));
+  const int pc = lane & 15;
+  // group-A wave `wave` loads keys 16 wave .. 16 wave + 15 of block blk: load i covers keys
+  // 16 wave + 4 i + lane / 16 (1 KB of K, 1 KB of V), LDS chunk lane % 16 of each key row
+  auto issue = [&](int blk) {
+    const uint32_t st_lds = smem_lds + uint32_t((blk % kLongStages) * kStageBytes);
+    const int n0 = k_begin + kTileN * blk;
+    int64_t slots[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      slots[i] = slot_of(min(n0 + 16 * wave + 4 * i + (lane >> 4), k_end - 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = 4 * wave + i;
+      const int key = 4 * q + (lane >> 4);
+      const uint16_t* ks = a.k + slots[i] * D + col0;
+      const uint16_t* vs = a.v + slots[i] * D + col0;
+      const int kc = pc ^ (key & 15), vc = pc ^ ((key & 7) << 1);
+      dma16(ks + 8 * kc, __builtin_amdgcn_readfirstlane(st_lds + 1024 * q));
+      dma16(vs + 8 * vc, __builtin_amdgcn_readfirstlane(st_lds + kTileBytes + 1024 * q));
+    }
+  };
+
+  LongState st;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    st.m[rb] = -INFINITY;
+    st.l[rb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
+  const float sl2 = a.scale_log2;
+  auto kt_of = [&](int p) {
+    return reinterpret_cast<const u32x4*>(smem + (p % kLongStages) * kStageBytes);
+  };
+  auto vt_of = [&](int p) -> const u32x4* { return vtb[p & 1]; };
+  auto transpose = [&](int p) {
+    transpose_v(smem + (p % kLongStages) * kStageBytes + kTileBytes, vtb[p & 1], wave, lane);
+  };
+
+  int issued = 0;
+  if (grp_a) {
+    const int np = min(n_blk, kLongStages);
+    for (int blk = 0; blk < np; ++blk) issue(blk);
+    issued = np;
+    if (np > 0) wait_loads(kLongLoads * (np - 1));  // block 0 landed
+  }
+  barrier_only();
+  if (n_blk > 0) {
+    f32x4 sc[2][4];
+    bf16x8 pb[2][2];
+    if (grp_a) {
+      auto run_a = [&](auto imp_tag) {
+        constexpr bool kImp = decltype(imp_tag)::value;
+        bf16x8 qs[4];
+        if constexpr (kImp) {
+#pragma unroll
+          for (int sd = 0; sd < 4; ++sd) qs[sd] = as_bf16x8(qsum_frag_buf[sd][lane]);
+        }
+        // raw importance of block p: wave w sums keys 16 w .. 16 w + 15
+        auto imp_block = [&](int p) {
+          if constexpr (kImp) {
+            const u32x4* kt = kt_of(p);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sd = 0; sd < 4; ++sd)
+              acc = mfma16(qs[sd], k_frag(kt, wave, sd, l16, g), acc);
+            const int n = k_begin + kTileN * p + 16 * wave + l16;
+            if (g == 0 && n < k_end) imp_out[slot_of(n)] = acc[0] + acc[1];
+          }
+        };
+        long_qk(sc, qf, kt_of(0), l16, g);
+        imp_block(0);
+        barrier_only();
+        if (n_blk == 1)
+          long_softmax<true>(st, sc, pb, sl2, k_end - k_begin, g);
+        else
+          long_softmax<false>(st, sc, pb, sl2, kTileN, g);
+        transpose(0);
+        if (n_blk > 1) wait_loads(kLongLoads * (issued - 2));  // block 1 landed
+        barrier_only();
+        for (int p = 1; p < n_blk - 1; ++p) {
+          if (p + 2 < n_blk) {
+            issue(p + 2);  // into the stage of block p - 1, released by the last barrier
+            ++issued;
+          }
+          long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
+          imp_block(p);
+          barrier_only();
+          long_softmax<false>(st, sc, pb, sl2, kTileN, g);
+          transpose(p);
+          wait_loads(kLongLoads * (issued - p - 2));  // block p + 1 landed
+          barrier_only();
+        }
+        if (n_blk > 1) {
+          const int p = n_blk - 1;
+          long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
+          imp_block(p);
+          barrier_only();
+          long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * p), g);
+          transpose(p);
+          barrier_only();
+        }
+        long_pv(st, pb, vt_of(n_blk - 1), lane);
+        barrier_only();
+        barrier_only();
+      };
+      if (imp_raw)
+        run_a(std::true_type{});
+      else
+        run_a(std::false_type{});
+    } else {
+      barrier_only();
+      long_qk(sc, qf, kt_of(0), l16, g);
+      barrier_only();
+      for (int p = 1; p < n_blk; ++p) {
+        long_softmax<false>(st, sc, pb, sl2, kTileN, g);
+        barrier_only();
+        long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
+        barrier_only();
+      }
+      long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * (n_blk - 1)), g);
+      barrier_only();
+      long_pv(st, pb, vt_of(n_blk - 1), lane);
+      barrier_only();
+    }
+  }
+  if (grp_a) wait_loads(0);  // no load may still be writing LDS when the workgroup ends
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    st.l[rb] = xsum(st.l[rb]);
+    if (qrow[rb] < 0) continue;
+    const float inv = st.l[rb] > 0.f ? 1.f / st.l[rb] : 0.f;
+    uint16_t* orow = a.out + qrow[rb] * D + col0;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const f32x4 o = st.o[rb][db];
+      const u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+      st8(orow + 16 * db + 4 * g, pk);
+    }
+  }
+}
+
 // scores[slot] += scale * sum_h imp_part[h][slot] over the keys of each importance tile;
 // blockIdx.y = work item, blockIdx.x strides over its keys.
 __global__ __launch_bounds__(256) void imp_accumulate_kernel(
@@ -645,8 +1095,8 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   using namespace fdl;
   FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
-  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128, FDL_ERR_UNSUPPORTED,
-              "fdl_block_attention: tile_rows = %d (64 or 128)", tile_rows);
+  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention: tile_rows = %d (64, 128 or 256)", tile_rows);
   if (n_work == 0) return ok();
   int rc = check_common("fdl_block_attention", q, k_cache, v_cache, out, d_model, n_heads,
                         head_dim);
@@ -684,9 +1134,25 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // 64-row tiles: four consumers of 16 rows; 128-row tiles: eight consumers (two per SIMD)
-  const hipError_t e = tile_rows == 64 ? launch_attn<1, 4, false>(args, n_work, n_heads, s)
-                                        : launch_attn<1, 8, false>(args, n_work, n_heads, s);
+  // 64-row tiles: four consumers of 16 rows; 128-row tiles: eight consumers (two per SIMD);
+  // 256-row tiles: the two-group kernel, or with softmax-colsum importance the 128-row
+  // kernel on each half of an item (the importance rows lie in the first half)
+  hipError_t e;
+  if (tile_rows == 64) {
+    e = launch_attn<1, 4, false>(args, n_work, n_heads, s);
+  } else if (tile_rows == 128) {
+    e = launch_attn<1, 8, false>(args, n_work, n_heads, s);
+  } else if (imp_mode == FDL_IMP_SOFTMAX_COLSUM) {
+    FDL_REQUIRE(n_work < (int64_t(1) << 30), FDL_ERR_SHAPE,
+                "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
+    args.split = 1;
+    e = launch_attn<1, 8, false>(args, 2 * n_work, n_heads, s);
+  } else {
+    hipLaunchKernelGGL(attn_long_kernel,
+                       dim3(static_cast<unsigned>(n_work), static_cast<unsigned>(n_heads)),
+                       dim3(64 * 8), 0, s, args);
+    e = hipGetLastError();
+  }
   FDL_HIP_CHECK(e);
   return ok();
 }

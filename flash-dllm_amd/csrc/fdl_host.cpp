@@ -82,8 +82,8 @@ extern "C" int fdl_validate_work(const int32_t* work, int64_t n_work, const int3
     FDL_REQUIRE(kb >= 0 && kb <= ke && ke <= max_pages * page, FDL_ERR_RANGE,
                 "fdl_validate_work: work %lld key range [%d, %d) outside [0, %lld)",
                 (long long)w, kb, ke, (long long)(max_pages * page));
-    FDL_REQUIRE(nr >= 1 && nr <= 128, FDL_ERR_RANGE,
-                "fdl_validate_work: work %lld has %d rows (1..128 allowed)", (long long)w, nr);
+    FDL_REQUIRE(nr >= 1 && nr <= 256, FDL_ERR_RANGE,
+                "fdl_validate_work: work %lld has %d rows (1..256 allowed)", (long long)w, nr);
     FDL_REQUIRE(ni >= 0 && ni <= nr, FDL_ERR_RANGE,
                 "fdl_validate_work: work %lld has n_imp %d outside [0, %d]", (long long)w, ni,
                 nr);

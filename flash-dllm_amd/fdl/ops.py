@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from . import lib as _lib
-from .schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, AttnPlan
+from .schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, MID_TILE_ROWS, AttnPlan
 
 BF16 = torch.bfloat16
 
@@ -106,9 +106,14 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     d_model = q.shape[1]
     stream = _stream(q)
     n_row_idx = max(int(plan.row_idx.size), 1)
-    # long-row tiles (the first n_long work items), then short-row tiles
+    if imp_mode == _lib.IMP_SOFTMAX_COLSUM and plan.n_long and int(plan.work[:plan.n_long, 5].max()) > MID_TILE_ROWS:
+        raise _lib.FdlError(_lib.FDL_ERR_UNSUPPORTED,
+                            f"softmax-colsum importance needs at most {MID_TILE_ROWS} importance rows per sequence")
+    # long tiles (the first n_long work items), mid tiles (the next n_mid), short tiles
+    n_short = plan.n_work - plan.n_long - plan.n_mid
     for first, count, tile_rows in ((0, plan.n_long, LONG_TILE_ROWS),
-                                    (plan.n_long, plan.n_work - plan.n_long, MAX_TILE_ROWS)):
+                                    (plan.n_long, plan.n_mid, MID_TILE_ROWS),
+                                    (plan.n_long + plan.n_mid, n_short, MAX_TILE_ROWS)):
         if count == 0:
             continue
         _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),

@@ -2,8 +2,8 @@
 
 The reference launches masked-block attention and tracked-block attention separately
 (flash_cache_triton.py:561-607), so every sequence's K/V are streamed twice. Here a
-sequence's masked rows and tracked rows are packed into the same tiles (up to 64 query
-rows per tile): masked rows first, so that the first `n_imp` rows of the sequence's first
+sequence's masked rows and tracked rows are packed into the same tiles (64, 128 or 256
+query rows per tile): masked rows first, so that the first `n_imp` rows of the sequence's first
 tile are the rows whose logits feed the importance scores (flash_cache_triton.py:155-158,
 :614-615).
 
@@ -20,7 +20,8 @@ import numpy as np
 import torch
 
 MAX_TILE_ROWS = 64        # rows per tile of the short-row variant
-LONG_TILE_ROWS = 128      # rows per tile of the long-row (full recompute) variant
+MID_TILE_ROWS = 128       # rows per tile of the mid-row variant (65..128 rows)
+LONG_TILE_ROWS = 256      # rows per tile of the long-row (full recompute) variant
 DEFAULT_PAGE_LOG2 = 5  # 32-slot pages
 
 
@@ -43,44 +44,53 @@ def contiguous_page_table(n_seq: int, max_length: int, page_log2: int = DEFAULT_
     return (np.arange(n_seq, dtype=np.int64)[:, None] * per + np.arange(per)[None, :]).astype(np.int32)
 
 
-def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS,
-               long_rows: int = LONG_TILE_ROWS) -> tuple[np.ndarray, np.ndarray, int]:
-    """Splits each sequence's rows into tiles.
+def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS, mid_rows: int = MID_TILE_ROWS,
+               long_rows: int = LONG_TILE_ROWS) -> tuple[np.ndarray, np.ndarray, int, int]:
+    """Splits each sequence's rows into tiles of three classes.
 
-    A sequence with more than `max_rows` rows is cut into tiles of up to `long_rows` rows
-    (the variant with two 16-row blocks per wavefront, for MFMA-bound full recomputes);
-    the others get one tile of up to `max_rows` rows. Returns (work int32 [n, 8],
-    row_idx int32, n_long): the first n_long work items are long-row tiles. Within each
-    class tiles are ordered longest first. The importance rows of a sequence must fit in
-    its first tile.
+    Up to `max_rows` rows: one short tile. Up to `mid_rows`: one mid tile. More (full
+    recomputes): tiles of `long_rows` rows, the last one with the remainder (a long tile
+    costs the same whatever its row count, but the classes are separate launches, and a
+    remainder in another class would run after the long tiles instead of among them).
+    Returns (work int32 [n, 8], row_idx int32, n_long, n_mid): the first n_long work items
+    are long tiles, the next n_mid mid tiles, the rest short tiles. Within each class
+    tiles are ordered longest first. The importance rows of a sequence must fit in its
+    first tile.
     """
-    items = [[], []]
+    items = [[], [], []]
     row_chunks = []
     off = 0
+    limits = (long_rows, mid_rows, max_rows)
+
+    def cls_of(n: int) -> int:
+        return 2 if n <= max_rows else (1 if n <= mid_rows else 0)
+
     for sq in seqs:
         rows = np.asarray(sq.rows, dtype=np.int32).reshape(-1)
-        cls = 0 if len(rows) > max_rows else 1
-        step = long_rows if cls == 0 else max_rows
-        if sq.n_imp > step:
-            raise ValueError(f"{sq.n_imp} importance rows do not fit one {step}-row tile")
         if sq.n_imp > len(rows):
             raise ValueError("n_imp exceeds the number of rows")
-        for t0 in range(0, len(rows), step):
-            chunk = rows[t0:t0 + step]
+        t0 = 0
+        cls = cls_of(len(rows))
+        while t0 < len(rows):
+            chunk = rows[t0:t0 + limits[cls]]
             n_imp = sq.n_imp if t0 == 0 else 0
+            if n_imp > len(chunk):
+                raise ValueError(f"{sq.n_imp} importance rows do not fit one {len(chunk)}-row tile")
             items[cls].append((sq.batch, sq.k_begin, sq.k_end, off, len(chunk), n_imp, 0, 0))
             row_chunks.append(chunk)
             off += len(chunk)
+            t0 += len(chunk)
     if not row_chunks:
-        return np.zeros((0, 8), dtype=np.int32), np.zeros(0, dtype=np.int32), 0
+        return np.zeros((0, 8), dtype=np.int32), np.zeros(0, dtype=np.int32), 0, 0
     row_idx = np.concatenate(row_chunks).astype(np.int32)
     parts = []
-    for it in items:
+    for cls, it in enumerate(items):
         w = np.asarray(it, dtype=np.int32).reshape(-1, 8)
-        # longest first: keys x 16-row groups
-        cost = (w[:, 2].astype(np.int64) - w[:, 1]) * ((w[:, 4].astype(np.int64) + 15) // 16)
+        # longest first: keys x 16-row groups (long tiles: keys; every row group is computed)
+        groups = 1 if cls == 0 else (w[:, 4].astype(np.int64) + 15) // 16
+        cost = (w[:, 2].astype(np.int64) - w[:, 1]) * groups
         parts.append(w[np.argsort(-cost, kind="stable")])
-    return np.ascontiguousarray(np.concatenate(parts)), row_idx, len(items[0])
+    return np.ascontiguousarray(np.concatenate(parts)), row_idx, len(items[0]), len(items[1])
 
 
 def seqs_from_reference_blocks(masked_blocks: np.ndarray, tracked_blocks: np.ndarray,
@@ -116,7 +126,8 @@ class AttnPlan:
     row_idx: np.ndarray
     page_table: np.ndarray
     page_log2: int
-    n_long: int = 0  # leading work items that are long-row (128-row) tiles
+    n_long: int = 0  # leading work items that are long (256-row) tiles
+    n_mid: int = 0   # the next work items, mid (128-row) tiles
     work_d: torch.Tensor = field(repr=False, default=None)
     row_idx_d: torch.Tensor = field(repr=False, default=None)
     page_table_d: torch.Tensor = field(repr=False, default=None)
@@ -157,9 +168,9 @@ class AttnPlan:
 
 def make_plan(seqs: list[SeqRows], page_table: np.ndarray, page_log2: int = DEFAULT_PAGE_LOG2,
               device=None, max_rows: int = MAX_TILE_ROWS) -> AttnPlan:
-    work, row_idx, n_long = build_work(seqs, max_rows)
+    work, row_idx, n_long, n_mid = build_work(seqs, max_rows)
     plan = AttnPlan(work=work, row_idx=row_idx, page_table=np.ascontiguousarray(page_table, dtype=np.int32),
-                    page_log2=page_log2, n_long=n_long)
+                    page_log2=page_log2, n_long=n_long, n_mid=n_mid)
     if device is not None:
         plan.to(device)
     return plan

@@ -99,8 +99,10 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *   k_cache, v_cache bf16 [n_slots][d_model]
  *   page_table int32 [n_seq][max_pages]; page size 1 << page_log2 (4 <= page_log2 <= 12)
  *   work     int32 [n_work][8] (see above); row_idx int32 [n_row_idx]
- *   tile_rows 64 or 128: every work item of the call has at most tile_rows rows; 128 selects
- *            the variant for long (full-recompute) row sets, 64 the one for short ones
+ *   tile_rows 64, 128 or 256: every work item of the call has at most tile_rows rows; 256
+ *            selects the variant for full-recompute row sets, 128 and 64 the ones for mid and
+ *            short ones. With tile_rows 256 and FDL_IMP_SOFTMAX_COLSUM the importance rows
+ *            must lie in the first 128 rows of an item (n_imp <= 128).
  *   out      bf16 [n_q_rows][d_model]       rows named by row_idx are written
  *   imp_mode FDL_IMP_*; imp_part fp32 [n_heads][n_slots]: for every tile with n_imp > 0,
  *            imp_part[h][slot(n)] = sum over its first n_imp rows r of the head-h term

@@ -84,10 +84,31 @@ def test_validate_rows():
     lib.call("fdl_validate_rows", dp, None, 3, 3, 8, 1)
 
 
+def test_build_work_tile_classes():
+    """More than 128 rows: 256-row tiles (remainder included); up to 128: one 128-row tile;
+    up to 64: one 64-row tile. Importance rows stay in their sequence's first tile; every
+    row is covered once."""
+    seqs = [SeqRows(0, 600, np.arange(0, 600), 32), SeqRows(1, 300, np.arange(600, 900)),
+            SeqRows(2, 100, np.arange(900, 1000), 8), SeqRows(3, 50, np.arange(1000, 1040))]
+    work, rows, n_long, n_mid = build_work(seqs)
+    assert sorted(work[:n_long, 4].tolist()) == [44, 88, 256, 256, 256]
+    assert sorted(work[n_long:n_long + n_mid, 4].tolist()) == [100]
+    assert sorted(work[n_long + n_mid:, 4].tolist()) == [40]
+    assert sorted(rows.tolist()) == list(range(1040))
+    imp = work[work[:, 5] > 0]
+    assert sorted(imp[:, 5].tolist()) == [8, 32]
+    for it in imp:
+        first = {0: 0, 2: 900}[int(it[0])]
+        assert rows[it[3]] == first
+    with pytest.raises(ValueError):
+        build_work([SeqRows(0, 64, np.arange(0, 10), 11)])
+
+
 def test_validate_work():
     pt = contiguous_page_table(2, 128)
-    work, rows, n_long = build_work([SeqRows(0, 100, np.arange(0, 40), 8), SeqRows(1, 128, np.arange(40, 150))])
-    assert n_long == 1 and work[0, 4] == 110
+    work, rows, n_long, n_mid = build_work([SeqRows(0, 100, np.arange(0, 40), 8),
+                                            SeqRows(1, 128, np.arange(40, 150))])
+    assert n_long == 0 and n_mid == 1 and work[0, 4] == 110
     w, wp = _arr(work, np.int32)
     r, rp = _arr(rows, np.int32)
     p, pp = _arr(pt, np.int32)

@@ -240,6 +240,49 @@ def test_block_attention_paged_stress():
         _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"importance seq {sq.batch}")
 
 
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM])
+def test_block_attention_full_recompute_tiles(imp_mode):
+    """Full recomputes (q = k: 256-row tiles, with 188- and 1-row remainders) next to a
+    100-row (128-row class) and a 40-row (64-row class) sequence, ragged k_end, 32
+    importance rows per sequence."""
+    B, L, H = 5, 1024, 4
+    k_ends = [1024, 700, 513, 300, 200]
+    n_q = [1024, 700, 513, 100, 40]
+    seqs, blocks, mb, q0 = [], [], [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
+                            n_imp=32 if imp_mode else 0))
+        blocks.append((b, k_ends[b], q0, q0 + n_q[b]))
+        mb.append((b, k_ends[b], q0, q0 + 32))
+        q0 += n_q[b]
+    Q = q0
+    q, kc, vc = _attn_inputs(11, Q, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    assert plan.n_long == 10 and plan.n_mid == 1 and plan.n_work == 12
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(B * L, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode,
+                        imp if imp_mode else None)
+    if imp_mode:
+        ops.importance_accumulate(imp, plan, 1.0 / (32 * H) if imp_mode == lib.IMP_RAW_LOGIT else 1.0,
+                                  scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    ref = orc.block_attention(qn, kn, vn, np.array(blocks), L, H, scale)
+    _close(_np(out), ref, what="attention out")
+    mb = np.array(mb)
+    if imp_mode == lib.IMP_RAW_LOGIT:
+        S = orc.importance_raw_S(qn, kn, mb, B, L, H, 32)
+        exp = orc.importance_accumulate(np.zeros(B * L, np.float32), S)
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="raw importance")
+    elif imp_mode == lib.IMP_SOFTMAX_COLSUM:
+        exp = orc.importance_softmax_colsum(qn, kn, mb, B, L, H, scale)
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
+
+
 def test_block_attention_leaves_other_rows_untouched():
     B, L, H = 2, 128, 2
     seqs = [SeqRows(0, 100, np.array([5, 1, 9])), SeqRows(1, 128, np.array([0, 7]))]
