@@ -601,18 +601,20 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
 // half-step each SIMD has one wavefront issuing MFMAs and one running the softmax:
 //   half-step 2j:     A: M_j                        B: V_{j-1}
 //   half-step 2j + 1: A: V_j + transpose of V_j    B: M_j
-// with a workgroup barrier between half-steps. Group A also moves the blocks: it issues the
-// global -> LDS loads of block j + 2 at the start of M_j into a three-deep ring (K and
-// row-major V of a block, 32 KB) and rewrites each V block, after its softmax, into a
-// fragment-major V^T buffer (two, by block parity) from which both groups read the
-// O^T = V^T P^T operands with one 16-byte read per lane instead of two transposing reads.
+// with a workgroup barrier between half-steps. Blocks move into a three-deep LDS ring (K and
+// row-major V of a block, 32 KB): in pair j each wavefront issues its quarter-block share of
+// the global -> LDS loads of block j + 2 at the start of its softmax phase, where it has
+// slack (an MFMA phase would stall on the issue). Group A rewrites each V block, after its
+// softmax, into a fragment-major V^T buffer (two, by block parity) from which both groups
+// read the O^T = V^T P^T operands with one 16-byte read per lane instead of two transposing
+// reads.
 //
 // The loads are issued from inline assembly: the compiler then does not know them and
 // inserts no wait for them before unrelated LDS reads; the waves wait for their own loads
 // explicitly (s_waitcnt vmcnt) before the barrier that hands a block to the readers.
 constexpr int kLongRows = 256;
 constexpr int kLongStages = 3;
-constexpr int kLongLoads = 8;  // 1 KB loads per group-A wavefront per block (4 K + 4 V)
+constexpr int kLongLoads = 4;  // 1 KB loads per wavefront per block (2 K + 2 V)
 
 // 16 bytes per lane from global memory into LDS at lds + 16 * lane (lds wavefront-uniform).
 // M0 carries the LDS address; its previous value is restored.
@@ -629,12 +631,12 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
       : "memory");
 }
 
-// Waits until at most n of this wavefront's global loads are outstanding (n = 0, 8, 16).
+// Waits until at most n of this wavefront's global loads are outstanding (n = 0, 4, 8).
 __device__ __forceinline__ void wait_loads(int n) {
   switch (n) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
   }
 }
 
@@ -882,18 +884,33 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
 
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_ptr)smem));
   const int pc = lane & 15;
-  // group-A wave `wave` loads keys 16 wave .. 16 wave + 15 of block blk: load i covers keys
-  // 16 wave + 4 i + lane / 16 (1 KB of K, 1 KB of V), LDS chunk lane % 16 of each key row
+  // wave w loads keys 8 w .. 8 w + 7 of block blk: load i covers keys 8 w + 4 i + lane / 16
+  // (1 KB of K, 1 KB of V), LDS chunk lane % 16 of each key row. When those 8 keys share a
+  // page (k_begin % 8 == 0) their slots come from one scalar page-table load; keys past
+  // k_end repeat the last key.
+  const bool scalar_pages = (k_begin & 7) == 0 && pl >= 3;
+  const int64_t slot_last = n_blk > 0 ? lookup(k_end - 1) : 0;
   auto issue = [&](int blk) {
     const uint32_t st_lds = smem_lds + uint32_t((blk % kLongStages) * kStageBytes);
     const int n0 = k_begin + kTileN * blk;
-    int64_t slots[4];
+    int64_t slots[2];
+    if (scalar_pages) {
+      const int nf = __builtin_amdgcn_readfirstlane(n0 + 8 * wave);
+      const int64_t base = nf < k_end ? int64_t(ptab[nf >> pl]) << pl : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      slots[i] = slot_of(min(n0 + 16 * wave + 4 * i + (lane >> 4), k_end - 1));
+      for (int i = 0; i < 2; ++i) {
+        const int n = nf + 4 * i + (lane >> 4);
+        const int64_t s = base | (n & pmask);
+        slots[i] = n < k_end && s >= 0 && s < n_slots ? s : slot_last;
+      }
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = 4 * wave + i;
+      for (int i = 0; i < 2; ++i)
+        slots[i] = slot_of(min(n0 + 8 * wave + 4 * i + (lane >> 4), k_end - 1));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = 2 * wave + i;
       const int key = 4 * q + (lane >> 4);
       const uint16_t* ks = a.k + slots[i] * D + col0;
       const uint16_t* vs = a.v + slots[i] * D + col0;
@@ -921,13 +938,14 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
     transpose_v(smem + (p % kLongStages) * kStageBytes + kTileBytes, vtb[p & 1], wave, lane);
   };
 
-  int issued = 0;
-  if (grp_a) {
+  {
     const int np = min(n_blk, kLongStages);
     for (int blk = 0; blk < np; ++blk) issue(blk);
-    issued = np;
     if (np > 0) wait_loads(kLongLoads * (np - 1));  // block 0 landed
   }
+  // at the end of pair p each wave waits for its share of block p + 1 (block p + 2 may still
+  // be in flight); the barrier that follows hands block p + 1 to all readers
+  auto wait_next = [&](int p) { wait_loads(p + 2 < n_blk ? kLongLoads : 0); };
   barrier_only();
   if (n_blk > 0) {
     f32x4 sc[2][4];
@@ -960,19 +978,16 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
         else
           long_softmax<false>(st, sc, pb, sl2, kTileN, g);
         transpose(0);
-        if (n_blk > 1) wait_loads(kLongLoads * (issued - 2));  // block 1 landed
+        if (n_blk > 1) wait_next(0);
         barrier_only();
         for (int p = 1; p < n_blk - 1; ++p) {
-          if (p + 2 < n_blk) {
-            issue(p + 2);  // into the stage of block p - 1, released by the last barrier
-            ++issued;
-          }
           long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
           imp_block(p);
           barrier_only();
+          if (p + 2 < n_blk) issue(p + 2);  // into the stage of block p - 1, released in pair p - 1
           long_softmax<false>(st, sc, pb, sl2, kTileN, g);
           transpose(p);
-          wait_loads(kLongLoads * (issued - p - 2));  // block p + 1 landed
+          wait_next(p);
           barrier_only();
         }
         if (n_blk > 1) {
@@ -995,11 +1010,14 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
     } else {
       barrier_only();
       long_qk(sc, qf, kt_of(0), l16, g);
+      if (n_blk > 1) wait_next(0);
       barrier_only();
       for (int p = 1; p < n_blk; ++p) {
+        if (p + 2 < n_blk) issue(p + 2);
         long_softmax<false>(st, sc, pb, sl2, kTileN, g);
         barrier_only();
         long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
+        if (p + 1 < n_blk) wait_next(p);
         barrier_only();
       }
       long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * (n_blk - 1)), g);
@@ -1008,7 +1026,7 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
       barrier_only();
     }
   }
-  if (grp_a) wait_loads(0);  // no load may still be writing LDS when the workgroup ends
+  wait_loads(0);  // no load may still be writing LDS when the workgroup ends
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     st.l[rb] = xsum(st.l[rb]);
