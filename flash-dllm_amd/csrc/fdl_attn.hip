@@ -81,6 +81,7 @@ struct AttnArgs {
   int imp_mode;
   float scale_log2;  // softmax_scale * log2(e)
   int split;         // 1: workgroup 2i + j runs rows [128 j, 128 j + 128) of 256-row item i
+  int n_items;       // long tiles: work items of the launch (grid = n_items x heads)
 };
 
 template <int RB>
@@ -792,11 +793,18 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const bool grp_a = wave < 4;
   const int l16 = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y;
+  // One-dimensional grid of items x heads. Workgroup i runs on XCD i % 8: renumber so that
+  // each XCD gets a contiguous run of (head-major, item-minor) work, i.e. the tiles of one
+  // sequence and head run on one XCD at about the same time and share its L2 for K and V.
+  const int nwg = static_cast<int>(gridDim.x);
+  int wid = static_cast<int>(blockIdx.x);
+  if ((nwg & 7) == 0) wid = (wid & 7) * (nwg >> 3) + (wid >> 3);
+  const int item = wid % a.n_items;
+  const int h = wid / a.n_items;
   const int64_t D = a.d_model;
   const int col0 = h * kHeadDim;
 
-  const int32_t* it = a.work + 8 * blockIdx.x;
+  const int32_t* it = a.work + 8 * item;
   int b = it[0], k_begin = it[1], k_end = it[2], roff = it[3], n_rows = it[4];
   int n_imp = a.imp_mode ? it[5] : 0;
   if (b < 0 || b >= a.n_seq || k_begin < 0 ||
@@ -1166,8 +1174,11 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
     args.split = 1;
     e = launch_attn<1, 8, false>(args, 2 * n_work, n_heads, s);
   } else {
-    hipLaunchKernelGGL(attn_long_kernel,
-                       dim3(static_cast<unsigned>(n_work), static_cast<unsigned>(n_heads)),
+    FDL_REQUIRE(n_work * n_heads < (int64_t(1) << 31), FDL_ERR_SHAPE,
+                "fdl_block_attention: %lld items x %lld heads out of range", (long long)n_work,
+                (long long)n_heads);
+    args.n_items = static_cast<int>(n_work);
+    hipLaunchKernelGGL(attn_long_kernel, dim3(static_cast<unsigned>(n_work * n_heads)),
                        dim3(64 * 8), 0, s, args);
     e = hipGetLastError();
   }
