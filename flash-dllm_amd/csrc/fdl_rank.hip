@@ -6,22 +6,22 @@
 // resolved so that among equal scores the lower slot ranks higher (it sits later in the
 // ascending order), which makes the result a total order.
 //
-// One workgroup (1024 threads) per segment. Each entry becomes a 64-bit key
+// One workgroup per segment. Each entry becomes a 64-bit key
 //   (orderable(score) << 32) | (0xffffffff - slot)
 // whose ascending order is (score ascending, slot descending); the segment is padded to
-// 1024 * R keys with all-ones keys (they sort last) and bitonic-sorted with thread t holding
-// keys t*R .. t*R + R - 1 in registers. Compare-exchange steps whose stride is below R run
-// inside a thread, strides R .. 32R are lane exchanges within a wavefront, and only the
-// strides of 64R and above (10 of the 55 steps for 1024 keys) go through LDS
-// with a workgroup barrier. Sixteen wavefronts per segment hide the latency of the
-// exchange steps.
+// T * R keys (T threads, R keys each, a power of two) with all-ones keys (they sort last) and
+// bitonic-sorted with thread t holding keys t*R .. t*R + R - 1 in registers. The network is
+// unrolled at compile time: compare-exchange steps whose stride is below R run inside a
+// thread, strides R .. 32R are lane exchanges within a wavefront (DPP quad permutes for
+// lanes 1 and 2 apart, ds_swizzle for 4, 8 and 16, a lane permute for 32), and only the
+// strides of 64R and above go through LDS with a workgroup barrier (3 of the 55 steps for
+// 1024 keys with 256 threads of 4 keys).
 #include "fdl_device.h"
 #include "fdl_host.h"
 
 namespace fdl {
 namespace {
 
-constexpr int kThreads = 1024;
 constexpr int kMaxLen = 8192;  // 1024 threads x 8 keys
 
 // Monotone map float -> uint32 (x < y  <=>  ord(x) < ord(y)); -0.0 and +0.0 map together.
@@ -31,9 +31,27 @@ __device__ __forceinline__ uint32_t orderable(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
-  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), mask);
-  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), mask);
+// The value of lane (lane ^ M) of the wavefront.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  const int x = static_cast<int>(v);
+  if constexpr (M == 1) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  } else if constexpr (M == 4 || M == 8 || M == 16) {
+    // bit mode: lane i of each 32-lane half reads lane ((i & 0x1f) | 0) ^ M
+    return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(x, 0x1f | (M << 10)));
+  } else {
+    static_assert(M == 32, "lane distance");
+    return static_cast<uint32_t>(__shfl_xor(x, 32));
+  }
+}
+
+template <int M>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  const uint32_t lo = xor_lane<M>(static_cast<uint32_t>(v));
+  const uint32_t hi = xor_lane<M>(static_cast<uint32_t>(v >> 32));
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
@@ -46,19 +64,70 @@ __device__ __forceinline__ uint64_t cx(uint64_t mine, uint64_t other, int i, int
   return take_min ? (mine < other ? mine : other) : (mine < other ? other : mine);
 }
 
-template <int R>
-__global__ __launch_bounds__(kThreads) void rank_kernel(const float* __restrict__ scores,
-                                                        int64_t n_scores, int64_t* slots,
-                                                        int64_t n_slot_entries,
-                                                        const int32_t* __restrict__ seg,
-                                                        int max_len, int64_t* topk_out, int k) {
-  constexpr int P = kThreads * R;
+// One compare-exchange step (bitonic block size K, stride J) over the R keys of each thread.
+template <int T, int R, int K, int J>
+__device__ __forceinline__ void bitonic_step(uint64_t (&key)[R], int tid, uint64_t (*xbuf)[T * R],
+                                             int& buf) {
+  if constexpr (J >= 64 * R) {
+    // partner in another wavefront: exchange through LDS (two buffers, so one barrier
+    // separates a step's reads from the next step's writes)
+#pragma unroll
+    for (int r = 0; r < R; ++r) xbuf[buf][tid * R + r] = key[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = tid * R + r;
+      key[r] = cx(key[r], xbuf[buf][i ^ J], i, J, K);
+    }
+    buf ^= 1;
+  } else if constexpr (J >= R) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = tid * R + r;
+      key[r] = cx(key[r], xor_lane64<J / R>(key[r]), i, J, K);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int rp = r ^ J;
+      if (rp > r) {
+        const int i = tid * R + r;
+        const uint64_t lo = cx(key[r], key[rp], i, J, K);
+        const uint64_t hi = cx(key[rp], key[r], i ^ J, J, K);
+        key[r] = lo;
+        key[rp] = hi;
+      }
+    }
+  }
+}
+
+template <int T, int R, int K, int J>
+__device__ __forceinline__ void bitonic_merge(uint64_t (&key)[R], int tid,
+                                              uint64_t (*xbuf)[T * R], int& buf) {
+  bitonic_step<T, R, K, J>(key, tid, xbuf, buf);
+  if constexpr (J > 1) bitonic_merge<T, R, K, J / 2>(key, tid, xbuf, buf);
+}
+
+template <int T, int R, int K>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&key)[R], int tid, uint64_t (*xbuf)[T * R],
+                                             int& buf) {
+  bitonic_merge<T, R, K, K / 2>(key, tid, xbuf, buf);
+  if constexpr (K < T * R) bitonic_sort<T, R, 2 * K>(key, tid, xbuf, buf);
+}
+
+template <int T, int R>
+__global__ __launch_bounds__(T) void rank_kernel(const float* __restrict__ scores,
+                                                 int64_t n_scores, int64_t* slots,
+                                                 int64_t n_slot_entries,
+                                                 const int32_t* __restrict__ seg, int max_len,
+                                                 int64_t* topk_out, int k) {
+  constexpr int P = T * R;
   __shared__ uint64_t xbuf[2][P];
   const int s = blockIdx.x;
   const int64_t start = seg[2 * s];
   int len = seg[2 * s + 1];
   // a segment longer than max_len (rejected by the host) is left as is
-  if (start < 0 || len < 0 || len > max_len || start + len > n_slot_entries) len = 0;
+  if (start < 0 || len < 0 || len > max_len || len > P || start + len > n_slot_entries) len = 0;
   const int tid = threadIdx.x;
 
   uint64_t key[R];
@@ -76,48 +145,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const float* __restrict_
   }
 
   int buf = 0;
-  for (int kk = 2; kk <= P; kk <<= 1) {
-    for (int j = kk >> 1; j > 0; j >>= 1) {
-      if (j >= 64 * R) {
-        // partner in another wavefront: exchange through LDS (two buffers, so one barrier
-        // separates a step's reads from the next step's writes)
-#pragma unroll
-        for (int r = 0; r < R; ++r) xbuf[buf][tid * R + r] = key[r];
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const int i = tid * R + r;
-          key[r] = cx(key[r], xbuf[buf][i ^ j], i, j, kk);
-        }
-        buf ^= 1;
-      } else if (j >= R) {
-        const int lane_mask = j / R;  // partner lane within the wavefront
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const int i = tid * R + r;
-          key[r] = cx(key[r], shfl_xor64(key[r], lane_mask), i, j, kk);
-        }
-      } else {
-        // partner register of the same thread (j < R: unrolled over the possible strides so
-        // that every register index is a constant)
-#pragma unroll
-        for (int jj = R / 2; jj >= 1; jj >>= 1) {
-          if (j != jj) continue;
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const int rp = r ^ jj;
-            if (rp > r) {
-              const int i = tid * R + r;
-              const uint64_t lo = cx(key[r], key[rp], i, jj, kk);
-              const uint64_t hi = cx(key[rp], key[r], i ^ jj, jj, kk);
-              key[r] = lo;
-              key[rp] = hi;
-            }
-          }
-        }
-      }
-    }
-  }
+  bitonic_sort<T, R, 2>(key, tid, xbuf, buf);
 
   // key[r] is now element tid * R + r of the ascending order
 #pragma unroll
@@ -131,15 +159,15 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const float* __restrict_
     }
   }
   if (topk_out) {
-    for (int j = len + tid; j < k; j += kThreads) topk_out[int64_t(s) * k + j] = -1;
+    for (int j = len + tid; j < k; j += T) topk_out[int64_t(s) * k + j] = -1;
   }
 }
 
-template <int R>
+template <int T, int R>
 hipError_t launch_rank(int64_t n_seg, hipStream_t st, const float* scores, int64_t n_scores,
                        int64_t* slots, int64_t n_slot_entries, const int32_t* seg, int max_len,
                        int64_t* topk_out, int k) {
-  hipLaunchKernelGGL(rank_kernel<R>, dim3(static_cast<unsigned>(n_seg)), dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((rank_kernel<T, R>), dim3(static_cast<unsigned>(n_seg)), dim3(T), 0, st,
                      scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
   return hipGetLastError();
 }
@@ -167,15 +195,19 @@ extern "C" int fdl_importance_rank(const float* scores, int64_t n_scores, int64_
               "fdl_importance_rank: topk_out is NULL with k = %d", k);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
-  const int keys_per_thread = (max_len + kThreads - 1) / kThreads;
-  if (keys_per_thread <= 1)
-    e = launch_rank<1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (keys_per_thread <= 2)
-    e = launch_rank<2>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (keys_per_thread <= 4)
-    e = launch_rank<4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  // four keys per thread up to 4096 keys, eight beyond; threads rounded up to a power of two
+  if (max_len <= 256)
+    e = launch_rank<64, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (max_len <= 512)
+    e = launch_rank<128, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (max_len <= 1024)
+    e = launch_rank<256, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (max_len <= 2048)
+    e = launch_rank<512, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+  else if (max_len <= 4096)
+    e = launch_rank<1024, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
   else
-    e = launch_rank<8>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+    e = launch_rank<1024, 8>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
   FDL_HIP_CHECK(e);
   return ok();
 }

@@ -301,16 +301,19 @@ def test_block_attention_leaves_other_rows_untouched():
 
 # ------------------------------------------------------------------------- ranking
 
-def test_importance_rank_bit_exact():
+@pytest.mark.parametrize("L", [200, 500, 896, 2000, 4000])
+def test_importance_rank_bit_exact(L):
+    """Every sort-network size (256 .. 4096 keys), ragged segments incl. 0 and 1 entries,
+    many ties and signed zeros."""
     rng = np.random.default_rng(9)
-    B, L = 8, 896
+    B = 8
     scores = (rng.integers(-40, 40, B * L).astype(np.float32) * np.float32(0.25))
     scores[rng.choice(B * L, 50)] = -0.0
     full_pos = np.arange(B * L, dtype=np.int64).reshape(B, L)
     for b in range(B):
         full_pos[b] = full_pos[b][rng.permutation(L)]
     lens = [int(rng.integers(0, L)) for _ in range(B)]
-    lens[0], lens[1] = 0, 1
+    lens[0], lens[1], lens[2] = 0, 1, L - 1  # L - 1 selects the network size
     seg = np.array([[b * L, lens[b]] for b in range(B)], np.int32)
     k = 32
     slots_d = torch.from_numpy(full_pos.copy()).to(DEV)
