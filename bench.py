@@ -289,19 +289,20 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
     # --- Flash-Verify
     NV, LC, BMV = 16, 1024, 32
     kv = rng.integers(4, 33, NV)
-    rows = 2 * BMV
+    rows = 2 * BMV  # mask rows per verify block
     key_pos, vblocks, masks, qslots = [], [], [], []
-    k0 = 0
+    k0 = q0 = 0
     for b in range(NV):
         S = int(min(kv[b], BMV))
         cand = b * LC + 512 + np.arange(S)
         keys = np.setdiff1d(b * LC + np.arange(LC), cand)
         key_pos.append(keys)
-        vblocks.append([k0, k0 + len(keys), b * rows, b * rows + 2 * S])
+        vblocks.append([k0, k0 + len(keys), q0, q0 + 2 * S])
         k0 += len(keys)
+        q0 += 2 * S
         masks.append(verify_mask(0, S, BMV))
-        qslots.append(np.concatenate([cand, cand, np.full(rows - 2 * S, cand[-1])]))
-    QV = NV * rows
+        qslots.append(np.concatenate([cand, cand]))  # draft rows, then mask rows
+    QV = q0
     xv = bf(QV, D)
     kcv, vcv = bf(NV * LC, D), bf(NV * LC, D)
     sinv = torch.from_numpy(np.tile(np.sin(ang[:LC]), (NV, 1)).astype(np.float32)).to(dev)
@@ -321,7 +322,7 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
     b_va = float((2.0 * (LC - sk) * D * 2 + (LC - sk) * 8 + 2 * (2 * sk) * D * 2).sum())
     out["flash_verify"] = {
         "workload": f"{NV} sequences, 1024-slot caches, {int(sk.sum())} candidates as draft "
-                    f"and mask rows ({QV} packed rows incl. padding)",
+                    f"and mask rows ({QV} packed rows)",
         "qkv_rope_cache_packed": {"us": round(t_vq, 2)},
         "verify_attention": {"us": round(t_va, 2), "GB/s": round(b_va / t_va / 1e3, 1),
                              "hbm_frac": round(b_va / t_va / 1e3 / PEAK_HBM_GBS, 4),

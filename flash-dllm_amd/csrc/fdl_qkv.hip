@@ -26,6 +26,7 @@
 //    workgroup so the launch covers the CUs; X and W tiles staged through LDS with the
 //    global loads kStages steps ahead in a ring of registers and the LDS fragment reads of
 //    the next half-step interleaved with the MFMAs of the current one.
+#include <atomic>
 #include <type_traits>
 
 #include "fdl_device.h"
@@ -502,6 +503,61 @@ QkvPlan qkv_plan(int64_t n_rows) {
   return {qkv_pc_kernel, kPcBM, kPcBP, kPcThreads};
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Rows handed to the weight-streaming kernel at the end of a producer/consumer launch: a
+// remainder of at most 64 rows that would otherwise open one more round of workgroups on
+// the device (one workgroup per CU). At 576 rows: 4 full tiles (one round, 54 us) plus a
+// 64-row stream (22 us) instead of 5 tiles in two rounds (108 us).
+int64_t qkv_tail_rows(int64_t n_rows, int64_t n_pairs) {
+  if (n_rows <= kPcBM) return 0;
+  const int64_t tail = n_rows % kPcBM;
+  if (tail == 0 || tail > 64) return 0;
+  const int64_t per_mtile = n_pairs / kPcBP;
+  const int64_t cus = device_cus();
+  const int64_t full = (n_rows / kPcBM) * per_mtile;
+  const bool new_round = (full + per_mtile + cus - 1) / cus > (full + cus - 1) / cus;
+  return new_round ? tail : 0;
+}
+
+// Launches `plan` over rows [r0, r0 + n) of the call described by `args`.
+hipError_t qkv_launch(const QkvPlan& plan, QkvArgs args, int64_t r0, int64_t n,
+                      hipStream_t stream) {
+  const int64_t D = args.d_model;
+  const int64_t n_pairs = 3 * int64_t(args.n_heads) * kHalf;  // a multiple of every plan's bp
+  args.x += r0 * D;
+  args.slot += r0;
+  if (args.rope_row) args.rope_row += r0;
+  args.q_out += r0 * D;
+  if (args.kv_packed) {
+    args.k_out += r0 * D;
+    args.v_out += r0 * D;
+    args.n_kv_rows = n;
+  }
+  args.n_rows = n;
+  const int64_t n_mtiles = (n + plan.bm - 1) / plan.bm;
+  const int64_t n_tiles = n_mtiles * (n_pairs / plan.bp);
+  if (n_tiles >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  args.n_mtiles = static_cast<int>(n_mtiles);
+  args.n_tiles = static_cast<int>(n_tiles);
+  hipLaunchKernelGGL(plan.kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(plan.threads), 0,
+                     stream, args);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace fdl
 
@@ -547,12 +603,9 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   FDL_REQUIRE_ALIGNED(wq, 16);
   FDL_REQUIRE_ALIGNED(wk, 16);
   FDL_REQUIRE_ALIGNED(wv, 16);
-  const QkvPlan plan = qkv_plan(n_rows);
-  const int64_t n_pairs = 3 * n_heads * kHalf;  // a multiple of every plan's bp
-  const int64_t n_mtiles = (n_rows + plan.bm - 1) / plan.bm;
-  const int64_t n_tiles = n_mtiles * (n_pairs / plan.bp);
-  FDL_REQUIRE(n_tiles < (int64_t(1) << 31), FDL_ERR_UNSUPPORTED,
-              "fdl_qkv_rope_cache: %lld rows is too many", (long long)n_rows);
+  FDL_REQUIRE((n_rows + 63) / 64 * (3 * n_heads * kHalf / 32) < (int64_t(1) << 31),
+              FDL_ERR_UNSUPPORTED, "fdl_qkv_rope_cache: %lld rows is too many",
+              (long long)n_rows);
   QkvArgs args;
   args.x = static_cast<const uint16_t*>(x);
   args.w[0] = static_cast<const uint16_t*>(wq);
@@ -570,11 +623,13 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   args.n_kv_rows = n_kv_rows;
   args.d_model = static_cast<int>(d_model);
   args.n_heads = static_cast<int>(n_heads);
-  args.n_mtiles = static_cast<int>(n_mtiles);
-  args.n_tiles = static_cast<int>(n_tiles);
+  args.n_mtiles = 0;
+  args.n_tiles = 0;
   args.kv_packed = kv_packed;
-  hipLaunchKernelGGL(plan.kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(plan.threads), 0,
-                     static_cast<hipStream_t>(stream), args);
-  FDL_HIP_CHECK(hipGetLastError());
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t tail = qkv_tail_rows(n_rows, 3 * n_heads * kHalf);
+  const int64_t head = n_rows - tail;
+  FDL_HIP_CHECK(qkv_launch(qkv_plan(head), args, 0, head, st));
+  if (tail > 0) FDL_HIP_CHECK(qkv_launch(qkv_plan(tail), args, head, tail, st));
   return ok();
 }

@@ -113,6 +113,26 @@ def test_qkv_rope_cache_ragged_rows_small_model(Q):
     assert np.all(_np(kc)[untouched] == POISON)
 
 
+@pytest.mark.parametrize("kv_packed", [False, True])
+def test_qkv_rope_cache_streamed_tail(kv_packed):
+    """576 rows at d_model 4096: four 128-row tiles fill one round of workgroups and the
+    last 64 rows go to the weight-streaming kernel in a second launch; both launches must
+    land their rows (Q, K/V rows or packed K/V) within tolerance."""
+    rng = np.random.default_rng(5)
+    Q, n_slots = 576, 2048
+    slots = rng.choice(n_slots, Q, replace=False)
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(5, 32, Q, n_slots, slots, kv_packed=kv_packed)
+    _close(_np(q), q_ref, what="Q")
+    if kv_packed:
+        _close(_np(kc), k_ref, what="K packed")
+        _close(_np(vc), v_ref, what="V packed")
+    else:
+        _close(_np(kc)[s], k_ref[s], what="K rows")
+        _close(_np(vc)[s], v_ref[s], what="V rows")
+        untouched = np.setdiff1d(np.arange(n_slots), s)
+        assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
+
+
 @pytest.mark.parametrize("Q", [64, 600])
 def test_qkv_packed_verify_mode(Q):
     rng = np.random.default_rng(3)
