@@ -336,6 +336,20 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
   const bool inblock = kVerify && n_rows > 0;
   const int n_steps = n_blk * (imp_soft ? 2 : 1) + (inblock ? 1 : 0);
+  // Step -> key block: the first pass walks the blocks forward, the second (softmax
+  // importance, K only) walks them backward, so it starts with the last kStages blocks of
+  // the first pass, which are still in LDS, and continues with the most recently read ones.
+  // Block j always lives in stage j % kStages; a resident block is not loaded again.
+  auto block_of = [&](int step) {
+    return imp_soft && step >= n_blk ? 2 * n_blk - 1 - step : step;
+  };
+  auto stage_of = [&](int step) { return block_of(step) % kStages; };
+  // DMA per producer for step `step` (0: past the end, or a block still resident)
+  auto loads = [&](int step) {
+    if (step >= n_steps) return 0;
+    if (!kVerify && step >= n_blk) return step - n_blk < kStages ? 0 : kDmaPerTile;
+    return 2 * kDmaPerTile;
+  };
 
   const int pl = a.page_log2;
   const int pmask = (1 << pl) - 1;
@@ -367,13 +381,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     // Load i of producer wr fills LDS bytes [1024 q, 1024 q + 1024) of a tile, q = 4 wr + i:
     // keys 4q .. 4q + 3; lane -> key 4q + lane / 16, LDS chunk lane % 16.
     const int pc = lane & 15;
-    auto issue = [&](int step, int stage) {
-      const int s = min(step, n_steps - 1);  // steps past the end repeat the last one
-      uint8_t* st = smem + stage * kStageBytes;
+    auto issue = [&](int s) {
+      if (loads(s) == 0) return;
+      uint8_t* st = smem + stage_of(s) * kStageBytes;
       const bool in_blk = kVerify && inblock && s == n_steps - 1;
       const bool k_only = !kVerify && s >= n_blk;
-      const int blk = k_only ? s - n_blk : s;
-      const int n0 = k_begin + kTileN * blk;
+      const int n0 = k_begin + kTileN * block_of(s);
 #pragma unroll
       for (int i = 0; i < kDmaPerTile; ++i) {
         const int q = kDmaPerTile * wr + i;
@@ -396,22 +409,16 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
                                            (lds_ptr)(st + kTileBytes + 1024 * q), 16, 0, 0);
       }
     };
-    // loads of one step (K only in the second pass)
-    auto loads = [&](int step) {
-      const int s = min(step, n_steps - 1);
-      return (!kVerify && s >= n_blk) ? kDmaPerTile : 2 * kDmaPerTile;
-    };
     if (n_steps > 0) {
-      for (int s = 0; s < kStages; ++s) issue(s, s);
+      for (int s = 0; s < kStages; ++s) issue(s);
       wait_vmcnt(loads(1) + loads(2) + loads(3));  // step 0 landed
     }
     barrier_only();  // #1
-    int stage = 0;
     for (int s = 0; s < n_steps; ++s) {
       wait_vmcnt(loads(s + 2) + loads(s + 3));  // step s + 1 landed
       barrier_only();  // consumers are done with step s
-      issue(s + kStages, stage);
-      stage = stage == kStages - 1 ? 0 : stage + 1;
+      // step s + kStages lives in the stage of step s (a resident block's stage is kept)
+      issue(s + kStages);
     }
     wait_vmcnt(0);  // no load may still be writing LDS when the workgroup ends
     return;
@@ -512,15 +519,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   }
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
-  int stage = 0;
   for (int s = 0; s < n_steps; ++s) {
+    const int stage = stage_of(s);
     const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
     const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
     const bool pass2 = !kVerify && s >= n_blk;
     const bool in_blk = kVerify && inblock && s == n_steps - 1;
-    const int blk = pass2 ? s - n_blk : s;
-    const int n0 = k_begin + kTileN * blk;
-    if (imp_soft && s > n_blk) flush_imp(s - 1, k_begin + kTileN * (s - 1 - n_blk));
+    const int n0 = k_begin + kTileN * block_of(s);
+    if (imp_soft && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
     if (in_blk) {
       const int br = a.block_rows;
       attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
@@ -583,9 +589,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       }
     }
     barrier_lds_drained();  // step s consumed; step s + 1 landed
-    stage = stage == kStages - 1 ? 0 : stage + 1;
   }
-  if (imp_soft && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * (n_blk - 1));
+  if (imp_soft && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
   if (!l_reduced) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
