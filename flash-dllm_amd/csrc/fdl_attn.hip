@@ -155,6 +155,26 @@ __device__ __forceinline__ bf16x8 vt_frag(const uint8_t* vt, int ks, int db, int
   return as_bf16x8(w);
 }
 
+// Sum over the first n rows of a tile (row_idx[roff ..]) of Q[row][col], in ascending row
+// order; eight rows' index and Q loads are in flight at a time.
+__device__ __forceinline__ float sum_q_rows(const AttnArgs& a, int roff, int n, int64_t D,
+                                           int col) {
+  float acc = 0.f;
+  for (int r0 = 0; r0 < n; r0 += 8) {
+    int64_t qr[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) qr[u] = r0 + u < n ? int64_t(a.row_idx[roff + r0 + u]) : -1;
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = qr[u] >= 0 && qr[u] < a.n_q_rows ? bf2f(a.q[qr[u] * D + col]) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (qr[u] >= 0 && qr[u] < a.n_q_rows) acc += v[u];
+  }
+  return acc;
+}
+
 // Running maxima are raised lazily: a row keeps its reference maximum until a block's
 // logits exceed it by more than kLazyMax (log2 domain, a factor of 256), so the rescale of
 // O and l is skipped for most blocks. Probabilities then stay below 256 (fp32 and bf16
@@ -163,11 +183,12 @@ constexpr float kLazyMax = 8.f;
 
 // One 64-key block of online softmax + PV for the wave's RB row blocks. bias(rb, kb, i) is
 // 0 when row block rb's lane row may attend key 16*kb + 4*(l/16) + i of the block and
-// -infinity when it may not.
-template <int RB, typename Bias>
+// -infinity when it may not; probs(rb, p, m) sees the block's fp32 probabilities of row
+// block rb relative to the reference maximum m (log2 domain).
+template <int RB, typename Bias, typename Probs>
 __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf)[RB][4],
                                              const u32x4* kt, const uint8_t* vt,
-                                             float scale_log2, Bias bias) {
+                                             float scale_log2, Bias bias, Probs probs) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
   f32x4 sc[RB][4];
@@ -216,6 +237,7 @@ __device__ __forceinline__ void attend_block(RowState<RB>& st, const bf16x8 (&qf
         psum += p;
       }
     st.l[rb] = st.l[rb] * alpha[rb] + psum;
+    probs(rb, sc[rb], m_use);  // p = 2^(logit - m_use) of the block, before the bf16 cast
   }
   if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
 #pragma unroll
@@ -273,19 +295,33 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
   }
 }
 
+// Softmax importance kept in LDS (kStore kernels): the probabilities of up to kStoreRows
+// importance rows over up to kStoreBlocks key blocks, as fp16, each block relative to the
+// row's reference maximum at that block; the column sums are formed once the rows'
+// log-sum-exp is known, so K is not read a second time.
+constexpr int kStoreRows = 32;
+constexpr int kStoreBlocks = 12;
+
 // Steps of a tile, the same sequence for producers and consumers (one barrier each):
 //   [0, n_blk)          cache blocks, K and V
-//   [n_blk, 2 n_blk)    softmax importance only: the cache blocks again, K only
+//   [n_blk, 2 n_blk)    softmax importance without the LDS store: the cache blocks again,
+//                       K only, last block first
 //   n_blk               verify only (when the block has rows): the in-block keys
-template <int RB, int NC, bool kVerify>
+template <int RB, int NC, bool kVerify, bool kStore = false>
 __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
   constexpr int kRows = 16 * RB * NC;
-  __shared__ __align__(1024) uint8_t smem[kStages * kStageBytes];
+  constexpr int kSt = kStore ? 3 : kStages;  // LDS ring depth (the store needs the room)
+  __shared__ __align__(1024) uint8_t smem[kSt * kStageBytes];
   __shared__ float imp_buf[2][NC][kTileN];  // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
-  __shared__ float qsum_buf[kHeadDim];        // raw importance: sum of the importance rows' Q
-  __shared__ u32x4 qsum_frag_buf[4][64];      // its MFMA A-operand fragments, by lane
+  // raw importance: sum of the importance rows' Q and its MFMA A-operand fragments, by lane
+  __shared__ float qsum_buf[kStore ? 1 : kHeadDim];
+  __shared__ u32x4 qsum_frag_buf[kStore ? 1 : 4][64];
+  // kStore: fp16 probabilities [block][row][key] (8-byte units XOR-swizzled by row) and the
+  // rows' reference maxima [block][row]
+  __shared__ __align__(16) uint16_t prob_buf[kStore ? kStoreBlocks * kStoreRows * kTileN : 4];
+  __shared__ float pmax_buf[kStore ? kStoreBlocks * kStoreRows : 1];
 
   const int tid = threadIdx.x;
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
@@ -331,24 +367,33 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
 
-  const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
+  const bool imp_raw = !kStore && !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
   const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
   const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
   const bool inblock = kVerify && n_rows > 0;
-  const int n_steps = n_blk * (imp_soft ? 2 : 1) + (inblock ? 1 : 0);
+  // softmax importance from the LDS store (one pass) or from a second pass over K
+  const bool store = kStore && imp_soft && n_imp <= kStoreRows && n_blk <= kStoreBlocks;
+  const bool two_pass = imp_soft && !store;
+  const int n_steps = n_blk * (two_pass ? 2 : 1) + (inblock ? 1 : 0);
   // Step -> key block: the first pass walks the blocks forward, the second (softmax
-  // importance, K only) walks them backward, so it starts with the last kStages blocks of
-  // the first pass, which are still in LDS, and continues with the most recently read ones.
-  // Block j always lives in stage j % kStages; a resident block is not loaded again.
+  // importance, K only) walks them backward, so it starts with the last kSt blocks of the
+  // first pass, which are still in LDS, and continues with the most recently read ones.
+  // Block j always lives in stage j % kSt; a resident block is not loaded again.
   auto block_of = [&](int step) {
-    return imp_soft && step >= n_blk ? 2 * n_blk - 1 - step : step;
+    return two_pass && step >= n_blk ? 2 * n_blk - 1 - step : step;
   };
-  auto stage_of = [&](int step) { return block_of(step) % kStages; };
+  auto stage_of = [&](int step) { return block_of(step) % kSt; };
   // DMA per producer for step `step` (0: past the end, or a block still resident)
   auto loads = [&](int step) {
     if (step >= n_steps) return 0;
-    if (!kVerify && step >= n_blk) return step - n_blk < kStages ? 0 : kDmaPerTile;
+    if (!kVerify && step >= n_blk) return step - n_blk < kSt ? 0 : kDmaPerTile;
     return 2 * kDmaPerTile;
+  };
+  // loads of steps (step, last] that may still be in flight once step `step` has landed
+  auto later_loads = [&](int step, int last) {
+    int n = 0;
+    for (int t = step + 1; t <= last; ++t) n += loads(t);
+    return n;
   };
 
   const int pl = a.page_log2;
@@ -410,15 +455,15 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       }
     };
     if (n_steps > 0) {
-      for (int s = 0; s < kStages; ++s) issue(s);
-      wait_vmcnt(loads(1) + loads(2) + loads(3));  // step 0 landed
+      for (int s = 0; s < kSt; ++s) issue(s);
+      wait_vmcnt(later_loads(0, kSt - 1));  // step 0 landed (steps 0 .. kSt - 1 issued)
     }
     barrier_only();  // #1
     for (int s = 0; s < n_steps; ++s) {
-      wait_vmcnt(loads(s + 2) + loads(s + 3));  // step s + 1 landed
+      wait_vmcnt(later_loads(s + 1, s + kSt - 1));  // step s + 1 landed
       barrier_only();  // consumers are done with step s
-      // step s + kStages lives in the stage of step s (a resident block's stage is kept)
-      issue(s + kStages);
+      // step s + kSt lives in the stage of step s (a resident block's stage is kept)
+      issue(s + kSt);
     }
     wait_vmcnt(0);  // no load may still be writing LDS when the workgroup ends
     return;
@@ -489,14 +534,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   // Raw importance is linear in Q: the column sums over the importance rows of Q K^T are
   // (sum of those rows' Q) K^T. The fp32 sum is split into bf16 hi + lo parts, rows 0 and 1
   // of one 16-row MFMA operand, so one wavefront per block computes all 64 sums.
-  if (imp_raw && tid < kHeadDim) {
-    float acc = 0.f;
-    for (int r = 0; r < n_imp; ++r) {
-      const int64_t qr = int64_t(a.row_idx[roff + r]);
-      if (qr >= 0 && qr < a.n_q_rows) acc += bf2f(a.q[qr * D + col0 + tid]);
-    }
-    qsum_buf[tid] = acc;
-  }
+  if (imp_raw && tid < kHeadDim) qsum_buf[tid] = sum_q_rows(a, roff, n_imp, D, col0 + tid);
   barrier_lds_drained();  // #0
   // A-operand fragment sd of the summed Q: row 0 (lane l16 == 0) the bf16 part, row 1 the
   // remainder, other rows zero; built once by wave sd.
@@ -526,7 +564,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     const bool pass2 = !kVerify && s >= n_blk;
     const bool in_blk = kVerify && inblock && s == n_steps - 1;
     const int n0 = k_begin + kTileN * block_of(s);
-    if (imp_soft && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
+    if (two_pass && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
     if (in_blk) {
       const int br = a.block_rows;
       attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
@@ -535,7 +573,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         return j < n_rows && r < br && a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0
                    ? 0.f
                    : -INFINITY;
-      });
+      }, [](int, const f32x4 (&)[4], float) {});
     } else if (!pass2) {
       // keys past k_end (the tail of the last block) get a -infinity bias
       const int n_left = k_end - n0;
@@ -545,8 +583,26 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
           kbias[kb][ii] = 16 * kb + 4 * g + ii < n_left ? 0.f : -INFINITY;
-      attend_block<RB>(st, qf, kt, vt, a.scale_log2,
-                       [&](int, int kb, int ii) { return kbias[kb][ii]; });
+      const int blk = block_of(s);
+      attend_block<RB>(
+          st, qf, kt, vt, a.scale_log2, [&](int, int kb, int ii) { return kbias[kb][ii]; },
+          [&](int rb, const f32x4 (&p)[4], float m_use) {
+            if constexpr (kStore) {
+              const int r = 16 * (wr * RB + rb) + l16;
+              if (store && r < kStoreRows) {
+                // row r, keys 16 kb + 4 g .. + 3: 8-byte unit 4 kb + g, swizzled by row
+                uint16_t* prow = prob_buf + (blk * kStoreRows + r) * kTileN;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                  u32x2 w;
+                  w[0] = pack_f16x2(p[kb][0], p[kb][1]);
+                  w[1] = pack_f16x2(p[kb][2], p[kb][3]);
+                  st8(prow + 4 * ((4 * kb + g) ^ ((r >> 1) & 15)), w);
+                }
+                if (g == 0) pmax_buf[blk * kStoreRows + r] = m_use;
+              }
+            }
+          });
       if (imp_raw && wr < 4) {
         // consumer wr < 4: the 16 keys of key block kb = wr
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -590,7 +646,29 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     }
     barrier_lds_drained();  // step s consumed; step s + 1 landed
   }
-  if (imp_soft && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
+  if (two_pass && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
+  if constexpr (kStore) {
+    if (store) {
+      // every block's probabilities, maxima and the rows' log-sum-exp are in LDS (the last
+      // step's barrier); column sums over the importance rows in ascending row order
+      const int nk = k_end - k_begin;
+      for (int k0 = 4 * tid; k0 < nk; k0 += 4 * 64 * NC) {
+        const int j = k0 / kTileN, u = (k0 % kTileN) / 4;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < n_imp; ++r) {
+          const float c = fast_exp2(pmax_buf[j * kStoreRows + r] - lse_buf[r]);
+          const u32x2 w = ld8(prob_buf + (j * kStoreRows + r) * kTileN + 4 * (u ^ ((r >> 1) & 15)));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] += c * f16_bits_to_f32(w[e >> 1], e & 1);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = k_begin + k0 + e;
+          if (n < k_end) imp_out[slot_of(n)] = acc[e];
+        }
+      }
+    }
+  }
   if (!l_reduced) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
@@ -860,14 +938,7 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
       qf[rb][sd] = as_bf16x8(v);
     }
   }
-  if (imp_raw && tid < kHeadDim) {
-    float acc = 0.f;
-    for (int r = 0; r < n_imp; ++r) {
-      const int64_t qr = int64_t(a.row_idx[roff + r]);
-      if (qr >= 0 && qr < a.n_q_rows) acc += bf2f(a.q[qr * D + col0 + tid]);
-    }
-    qsum_buf[tid] = acc;
-  }
+  if (imp_raw && tid < kHeadDim) qsum_buf[tid] = sum_q_rows(a, roff, n_imp, D, col0 + tid);
   __syncthreads();
   // raw importance: summed Q as bf16 hi + lo rows of one MFMA operand (see attn_kernel)
   if (imp_raw && wave < 4) {
@@ -1104,9 +1175,9 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
-template <int RB, int NC, bool kVerify>
+template <int RB, int NC, bool kVerify, bool kStore = false>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>),
+  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify, kStore>),
                      dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
                      dim3(64 * (NC + kProducers)), 0, s, args);
   return hipGetLastError();
@@ -1170,7 +1241,8 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   // kernel on each half of an item (the importance rows lie in the first half)
   hipError_t e;
   if (tile_rows == 64) {
-    e = launch_attn<1, 4, false>(args, n_work, n_heads, s);
+    e = imp_mode == FDL_IMP_SOFTMAX_COLSUM ? launch_attn<1, 4, false, true>(args, n_work, n_heads, s)
+                                           : launch_attn<1, 4, false>(args, n_work, n_heads, s);
   } else if (tile_rows == 128) {
     e = launch_attn<1, 8, false>(args, n_work, n_heads, s);
   } else if (imp_mode == FDL_IMP_SOFTMAX_COLSUM) {

@@ -44,6 +44,17 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
   return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
 }
 
+// fp32 -> fp16 pair (round to nearest even) as the bits of one 32-bit word, low half first;
+// the bits of half `hi` of such a word back to fp32.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t w, int hi) {
+  return static_cast<float>(
+      __builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w & 0xffffu)));
+}
+
 // D = A * B + C on one wavefront.
 //   16x16x32: lane l supplies A[l % 16][8 * (l / 16) + j] and B[8 * (l / 16) + j][l % 16],
 //             j = 0..7, and holds C[4 * (l / 16) + i][l % 16], i = 0..3.

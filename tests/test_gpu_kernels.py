@@ -303,6 +303,41 @@ def test_block_attention_full_recompute_tiles(imp_mode):
         _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
 
 
+def test_block_attention_softmax_importance_store_and_two_pass():
+    """64-row tiles with softmax-colsum importance on both of the kernel's paths: the
+    probabilities kept in LDS (at most 32 importance rows and 12 key blocks: 17 rows over
+    768 keys, 32 rows over one block) and the second pass over K (16 blocks; 48 rows)."""
+    B, L, H = 4, 1024, 4
+    k_ends = [1000, 500, 768, 64]
+    n_q = [50, 60, 40, 64]
+    n_imp = [32, 48, 17, 32]
+    seqs, blocks, mb, q0 = [], [], [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
+                            n_imp=n_imp[b]))
+        blocks.append((b, k_ends[b], q0, q0 + n_q[b]))
+        mb.append((b, k_ends[b], q0, q0 + n_imp[b]))
+        q0 += n_q[b]
+    Q = q0
+    q, kc, vc = _attn_inputs(12, Q, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    assert plan.n_long == 0 and plan.n_mid == 0 and plan.n_work == B
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(B * L, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale,
+                        lib.IMP_SOFTMAX_COLSUM, imp)
+    ops.importance_accumulate(imp, plan, 1.0, scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    _close(_np(out), orc.block_attention(qn, kn, vn, np.array(blocks), L, H, scale),
+           what="attention out")
+    exp = orc.importance_softmax_colsum(qn, kn, np.array(mb), B, L, H, scale)
+    _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
+
+
 def test_block_attention_leaves_other_rows_untouched():
     B, L, H = 2, 128, 2
     seqs = [SeqRows(0, 100, np.array([5, 1, 9])), SeqRows(1, 128, np.array([0, 7]))]
