@@ -156,20 +156,20 @@ __device__ __forceinline__ bf16x8 vt_frag(const uint8_t* vt, int ks, int db, int
 }
 
 // Sum over the first n rows of a tile (row_idx[roff ..]) of Q[row][col], in ascending row
-// order; eight rows' index and Q loads are in flight at a time.
+// order; 32 rows' index loads, then their Q loads, are in flight at a time.
 __device__ __forceinline__ float sum_q_rows(const AttnArgs& a, int roff, int n, int64_t D,
                                            int col) {
   float acc = 0.f;
-  for (int r0 = 0; r0 < n; r0 += 8) {
-    int64_t qr[8];
+  for (int r0 = 0; r0 < n; r0 += 32) {
+    int qr[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) qr[u] = r0 + u < n ? int64_t(a.row_idx[roff + r0 + u]) : -1;
-    float v[8];
+    for (int u = 0; u < 32; ++u) qr[u] = r0 + u < n ? a.row_idx[roff + r0 + u] : -1;
+    float v[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      v[u] = qr[u] >= 0 && qr[u] < a.n_q_rows ? bf2f(a.q[qr[u] * D + col]) : 0.f;
+    for (int u = 0; u < 32; ++u)
+      v[u] = qr[u] >= 0 && qr[u] < a.n_q_rows ? bf2f(a.q[int64_t(qr[u]) * D + col]) : 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 32; ++u)
       if (qr[u] >= 0 && qr[u] < a.n_q_rows) acc += v[u];
   }
   return acc;
@@ -318,6 +318,9 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   // raw importance: sum of the importance rows' Q and its MFMA A-operand fragments, by lane
   __shared__ float qsum_buf[kStore ? 1 : kHeadDim];
   __shared__ u32x4 qsum_frag_buf[kStore ? 1 : 4][64];
+  // raw importance of key k_begin + i, written to imp_part after the key loop (a consumer's
+  // global store inside the loop would wait behind the producers' loads)
+  __shared__ float raw_buf[kStore || kVerify ? 1 : kSlotCache];
   // kStore: fp16 probabilities [block][row][key] (8-byte units XOR-swizzled by row) and the
   // rows' reference maxima [block][row]
   __shared__ __align__(16) uint16_t prob_buf[kStore ? kStoreBlocks * kStoreRows * kTileN : 4];
@@ -610,7 +613,13 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         for (int sd = 0; sd < 4; ++sd)
           acc = mfma16(as_bf16x8(qsum_frag_buf[sd][lane]), k_frag(kt, wr, sd, l16, g), acc);
         const int n = n0 + 16 * wr + l16;
-        if (g == 0 && n < k_end) imp_out[slot_of(n)] = acc[0] + acc[1];  // rows hi + lo
+        if (g == 0 && n < k_end) {
+          const float v = acc[0] + acc[1];  // rows hi + lo
+          if constexpr (!kStore && !kVerify) {
+            if (slots_staged) raw_buf[n - k_begin] = v;
+            else imp_out[slot_of(n)] = v;
+          }
+        }
       }
       if (imp_soft && s == n_blk - 1) {
         // end of the first pass: the rows' log2-sum-exp for the second pass
@@ -647,6 +656,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     barrier_lds_drained();  // step s consumed; step s + 1 landed
   }
   if (two_pass && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
+  if constexpr (!kStore && !kVerify) {
+    if (imp_raw && slots_staged) {
+      // the last step's barrier made every block's sums visible
+      for (int i = tid; i < k_end - k_begin; i += 64 * NC) imp_out[slot_buf[i]] = raw_buf[i];
+    }
+  }
   if constexpr (kStore) {
     if (store) {
       // every block's probabilities, maxima and the rows' log-sum-exp are in LDS (the last
