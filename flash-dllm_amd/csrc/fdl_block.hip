@@ -104,6 +104,27 @@ __global__ __launch_bounds__(kEwThreads) void silu_mul_kernel(const uint16_t* __
   }
 }
 
+// Rows of a [gate | up] buffer: row r's gate at g + r * ld, its up at u + r * ld, its output
+// at out + r * 8 * w8 (w8 16-byte chunks per row).
+__global__ __launch_bounds__(kEwThreads) void silu_mul_rows_kernel(
+    const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, int64_t ld, int64_t w8,
+    int64_t n8, uint16_t* __restrict__ out) {
+  for (int64_t c = int64_t(blockIdx.x) * kEwThreads + threadIdx.x; c < n8;
+       c += int64_t(gridDim.x) * kEwThreads) {
+    const int64_t r = c / w8, j8 = c - r * w8;
+    const u32x4 a = ld16(g + r * ld + 8 * j8), b = ld16(u + r * ld + 8 * j8);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = bf_lo(a[j]), g1 = bf_hi(a[j]);
+      const float s0 = round_bf(g0 / (1.0f + expf(-g0)));
+      const float s1 = round_bf(g1 / (1.0f + expf(-g1)));
+      o[j] = pack_bf16x2(s0 * bf_lo(b[j]), s1 * bf_hi(b[j]));
+    }
+    st16(out + 8 * c, o);
+  }
+}
+
 }  // namespace
 }  // namespace fdl
 
@@ -163,6 +184,29 @@ extern "C" int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* o
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate),
                      static_cast<const uint16_t*>(up), n8, static_cast<uint16_t*>(out));
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}
+
+extern "C" int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_rows,
+                                 int64_t width, int64_t ld, void* out, void* stream) {
+  using namespace fdl;
+  FDL_REQUIRE(n_rows >= 0 && width >= 0 && width % 8 == 0 && ld % 8 == 0 && ld >= width,
+              FDL_ERR_UNSUPPORTED,
+              "fdl_silu_mul_rows: width = %lld, ld = %lld (multiples of 8, ld >= width)",
+              (long long)width, (long long)ld);
+  if (n_rows == 0 || width == 0) return ok();
+  FDL_REQUIRE_PTR(gate);
+  FDL_REQUIRE_PTR(up);
+  FDL_REQUIRE_PTR(out);
+  FDL_REQUIRE_ALIGNED(gate, 16);
+  FDL_REQUIRE_ALIGNED(up, 16);
+  FDL_REQUIRE_ALIGNED(out, 16);
+  const int64_t w8 = width / 8, n8 = n_rows * w8;
+  const int64_t blocks = std::min<int64_t>((n8 + kEwThreads - 1) / kEwThreads, 256 * 8);
+  hipLaunchKernelGGL(silu_mul_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads),
+                     0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate),
+                     static_cast<const uint16_t*>(up), ld, w8, n8, static_cast<uint16_t*>(out));
   FDL_HIP_CHECK(hipGetLastError());
   return ok();
 }

@@ -66,6 +66,27 @@ def _linear(i: int, o: int, device, dtype) -> nn.Linear:
     return nn.Linear(i, o, bias=False, device=device, dtype=dtype)
 
 
+def _share_gate_up(block: nn.Module) -> None:
+    """Puts ff_proj.weight and up_proj.weight (each [h, d]) into one [2h, d] buffer, up_proj's
+    rows right after ff_proj's, keeping their values; the block's MLP can then run both
+    projections as one GEMM."""
+    wg, wu = block.ff_proj.weight, block.up_proj.weight
+    buf = torch.cat([wg.detach(), wu.detach()], 0)
+    h = wg.shape[0]
+    block.ff_proj.weight = nn.Parameter(buf[:h], requires_grad=wg.requires_grad)
+    block.up_proj.weight = nn.Parameter(buf[h:], requires_grad=wu.requires_grad)
+
+
+@torch.no_grad()
+def fuse_gate_up_(model: nn.Module) -> nn.Module:
+    """Re-lays every block's ff_proj / up_proj weights out as one buffer (see _share_gate_up),
+    for models whose parameters were created or loaded elsewhere."""
+    for m in model.modules():
+        if hasattr(m, "ff_proj") and hasattr(m, "up_proj"):
+            _share_gate_up(m)
+    return model
+
+
 class LLaDALlamaBlock(nn.Module):
     def __init__(self, cfg: LLaDAConfig, layer_id: int, attention_fn: Callable, device=None,
                  dtype=None):
@@ -81,6 +102,7 @@ class LLaDALlamaBlock(nn.Module):
         self.attn_out = _linear(d, d, device, dtype)
         self.ff_proj = _linear(d, h, device, dtype)
         self.up_proj = _linear(d, h, device, dtype)
+        _share_gate_up(self)
         self.ff_out = _linear(h, d, device, dtype)
         self.act = nn.SiLU()
         self.dropout = nn.Identity()

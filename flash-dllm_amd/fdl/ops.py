@@ -216,11 +216,26 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16(bf16(silu(gate)) * up) (fdl_silu_mul)."""
-    _need(gate, "gate", BF16)
-    _need(up, "up", BF16, None, gate.device)
+    """bf16(bf16(silu(gate)) * up) (fdl_silu_mul). gate and up may also be [rows, width]
+    views with one common row stride and unit column stride, such as the two halves of a
+    [rows, 2 * width] product (fdl_silu_mul_rows); out is then a new contiguous tensor."""
     if up.shape != gate.shape:
         raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "up shape differs from gate")
+    if (gate.dim() == 2 and not gate.is_contiguous() and gate.stride(1) == 1
+            and up.stride() == gate.stride()):
+        for t, name in ((gate, "gate"), (up, "up")):
+            if t.device.type != "cuda" or t.dtype != BF16:
+                raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} must be a bf16 GPU tensor")
+        if up.device != gate.device:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "up is on another device than gate")
+        if out is None:
+            out = torch.empty(gate.shape, dtype=BF16, device=gate.device)
+        _need(out, "out", BF16, 2, gate.device)
+        _lib.call("fdl_silu_mul_rows", gate.data_ptr(), up.data_ptr(), gate.shape[0],
+                  gate.shape[1], gate.stride(0), out.data_ptr(), _stream(gate))
+        return out
+    _need(gate, "gate", BF16)
+    _need(up, "up", BF16, None, gate.device)
     if out is None:
         out = torch.empty_like(gate)
     _need(out, "out", BF16, None, gate.device)

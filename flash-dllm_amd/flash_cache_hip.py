@@ -40,6 +40,7 @@ import weakref
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 from fdl import lib as _lib
 from fdl import ops
@@ -103,6 +104,25 @@ def _norm(norm, x: torch.Tensor, checkpoint_fn) -> torch.Tensor:
     return ops.rms_norm(x.contiguous(), p[0], p[1])
 
 
+def _adjacent_gate_up(block) -> torch.Tensor | None:
+    """[2h, d] view over ff_proj.weight and up_proj.weight when up_proj's rows directly
+    follow ff_proj's in one buffer (as LLaDABlock parameters are laid out by
+    fdl.model.fuse_gate_up_), else None. Neither projection may have a bias."""
+    fp, up = block.ff_proj, block.up_proj
+    wg, wu = fp.weight, up.weight
+    if getattr(fp, "bias", None) is not None or getattr(up, "bias", None) is not None:
+        return None
+    if (wg.dim() != 2 or wg.shape != wu.shape or wg.dtype != wu.dtype or wg.device != wu.device
+            or not wg.is_contiguous() or not wu.is_contiguous()):
+        return None
+    if wu.data_ptr() != wg.data_ptr() + wg.numel() * wg.element_size():
+        return None
+    if wu.untyped_storage().data_ptr() != wg.untyped_storage().data_ptr():
+        return None
+    h, d = wg.shape
+    return torch.as_strided(wg, (2 * h, d), (d, 1))
+
+
 def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
     """attn_out + residual + SiLU-gated MLP + residual (flash_cache_triton.py:618-638)."""
     att = self.attn_out(att)
@@ -116,6 +136,17 @@ def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
         x = x + self.dropout(att)
         og_x = x
         x = ck(self.ff_norm, x) if ck is not None else self.ff_norm(x)
+    w_gu = _adjacent_gate_up(self)
+    if w_gu is not None and ck is None and isinstance(self.act, torch.nn.SiLU) \
+            and x.dtype == torch.bfloat16:
+        # one GEMM over the concatenated ff_proj / up_proj weights, then SiLU(gate) * up
+        # over the two halves of each output row
+        h = self.ff_proj.weight.shape[0]
+        gu = F.linear(x, w_gu)
+        x = ops.silu_mul(gu[:, :h], gu[:, h:])
+        x = self.ff_out(x)
+        x = self.dropout(x)
+        return (og_x + x).unsqueeze(0)
     x, x_up = self.ff_proj(x), self.up_proj(x)
     if ck is None and isinstance(self.act, torch.nn.SiLU) and x.dtype == torch.bfloat16:
         x = ops.silu_mul(x, x_up)

@@ -191,6 +191,16 @@ int fdl_rms_norm(const void* x, const void* residual, const void* weight, int64_
  */
 int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* out, void* stream);
 
+/*
+ * fdl_silu_mul_rows: the same over n_rows rows whose gate and up halves are strided views,
+ * e.g. the two halves of one [n_rows][2 * width] product of the concatenated ff_proj / up_proj
+ * weights (one GEMM instead of the two at flash_cache_triton.py:628):
+ *   out[r][c] = bf16(bf16(silu(gate[r * ld + c])) * up[r * ld + c]), out contiguous [n_rows][width].
+ *   width and ld multiples of 8, ld >= width; all pointers 16-byte aligned.
+ */
+int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_rows, int64_t width,
+                      int64_t ld, void* out, void* stream);
+
 /* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
  * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
 int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,

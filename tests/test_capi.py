@@ -64,6 +64,30 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 1,
             1.0, None, None)
     assert lib.load().fdl_last_error().decode().startswith("fdl_importance_accumulate")
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 12, 16, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 16, 8, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_silu_mul_rows", None, None, 4, 16, 32, None, None)
+    lib.call("fdl_silu_mul_rows", None, None, 0, 16, 32, None, None)  # zero rows: no-op
+
+
+def test_gate_up_weights_share_one_buffer():
+    """LLaDABlock lays ff_proj / up_proj out as one [2h, d] buffer (values kept), so the
+    block epilogue can run them as one GEMM; separate buffers are detected."""
+    import torch
+    import flash_cache_hip as fch
+    from fdl.model import LLaDAConfig, LLaDALlamaBlock, fuse_gate_up_
+    cfg = LLaDAConfig.llada_8b()
+    cfg.d_model, cfg.n_heads, cfg.mlp_hidden_size = 64, 1, 96
+    blk = LLaDALlamaBlock(cfg, 0, fch.flash_fused_elastic_cache)
+    w = fch._adjacent_gate_up(blk)
+    assert w is not None and w.shape == (192, 64)
+    assert torch.equal(w[:96], blk.ff_proj.weight) and torch.equal(w[96:], blk.up_proj.weight)
+    g0, u0 = blk.ff_proj.weight.detach().clone(), blk.up_proj.weight.detach().clone()
+    blk.up_proj.weight = torch.nn.Parameter(u0.clone())
+    assert fch._adjacent_gate_up(blk) is None
+    fuse_gate_up_(blk)
+    w = fch._adjacent_gate_up(blk)
+    assert w is not None and torch.equal(w[:96], g0) and torch.equal(w[96:], u0)
 
 
 def _arr(a, dt):

@@ -61,3 +61,41 @@ def test_silu_mul_matches_torch(n):
     got = ops.silu_mul(g, u)
     torch.cuda.synchronize()
     _check(got, ref, f"silu_mul n={n}")
+
+
+@pytest.mark.parametrize("rows,width", [(1, 8), (37, 4096), (512, 12288)])
+def test_silu_mul_rows_on_gate_up_halves(rows, width):
+    """fdl_silu_mul_rows on the two halves of one [rows, 2 * width] product (the fused
+    ff_proj / up_proj GEMM) against silu(gate) * up on contiguous copies."""
+    gen = torch.Generator().manual_seed(rows + width)
+    gu = (2.0 * torch.randn(rows, 2 * width, generator=gen)).to(torch.bfloat16).to(DEV)
+    gate, up = gu[:, :width], gu[:, width:]
+    ref = torch.nn.functional.silu(gate.contiguous()) * up.contiguous()
+    got = ops.silu_mul(gate, up)
+    torch.cuda.synchronize()
+    assert got.is_contiguous() and got.shape == (rows, width)
+    _check(got, ref, f"silu_mul_rows {rows}x{width}")
+
+
+def test_block_mlp_tail_fused_gate_up_matches_two_gemms():
+    """The block epilogue with adjacent ff_proj / up_proj weights (one GEMM) against the
+    same block with the weights in separate buffers (two GEMMs)."""
+    import flash_cache_hip as fch
+    from fdl.model import LLaDAConfig, LLaDALlamaBlock, random_init_
+    cfg = LLaDAConfig.llada_8b()
+    cfg.d_model, cfg.n_heads, cfg.mlp_hidden_size = 512, 4, 1536
+    blk = LLaDALlamaBlock(cfg, 0, fch.flash_fused_elastic_cache, device=DEV, dtype=torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.normal_(0.0, 0.05, generator=gen)
+    assert fch._adjacent_gate_up(blk) is not None
+    x = torch.randn(40, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    att = torch.randn(40, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    fused = fch.block_mlp_tail(blk, x, att)
+    blk.up_proj.weight = torch.nn.Parameter(blk.up_proj.weight.detach().clone())
+    assert fch._adjacent_gate_up(blk) is None
+    split = fch.block_mlp_tail(blk, x, att)
+    torch.cuda.synchronize()
+    # the GEMM library may order the reduction differently for the wider product
+    torch.testing.assert_close(fused.float(), split.float(), atol=2e-2, rtol=1e-2)
