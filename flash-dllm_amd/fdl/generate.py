@@ -225,11 +225,13 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         logits = logits[:n_masked_rows]
         stats.forwards += 1
         stats.rows += len(qpos)
-        p = F.softmax(logits.to(torch.float64), dim=-1)
-        x0_p_all, x0_all = torch.max(p, dim=-1)
+        if logits.dtype == torch.bfloat16 and logits.is_cuda and logits.shape[0] > 0:
+            x0_p_all, x0_all = ops.softmax_confidence(logits.contiguous())
+        else:
+            x0_p_all, x0_all = torch.max(F.softmax(logits.to(torch.float64), dim=-1), dim=-1)
         x0_p_all = x0_p_all.cpu().numpy()
         x0_all = x0_all.cpu().numpy()
-        del p, logits
+        del logits
 
         keep_num = [0] * B
         acc_masked = 0
@@ -309,7 +311,10 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 stats.rows += len(vq)
                 draft_rows = np.concatenate([np.arange(a + T, a + T + S) for (a, T, S) in verify_meta.values()])
                 draft_tok = _to_dev(np.concatenate(x_verify)[draft_rows], dev)
-                pv = F.softmax(vlog.to(torch.float64), dim=-1).gather(1, draft_tok[:, None]).view(-1)
+                if vlog.dtype == torch.bfloat16 and vlog.is_cuda:
+                    pv = ops.softmax_confidence(vlog.contiguous(), draft_tok)[0]
+                else:
+                    pv = F.softmax(vlog.to(torch.float64), dim=-1).gather(1, draft_tok[:, None]).view(-1)
                 pv = pv.cpu().numpy()
                 del vlog
             else:

@@ -95,6 +95,8 @@ SIGNATURES: dict[str, tuple] = {
     "fdl_silu_mul": (ctypes.c_int, [_p, _p, _i64, _p, _p]),  # gate, up, n, out, stream
     # gate, up, n_rows, width, ld, out, stream
     "fdl_silu_mul_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
+    # logits, n_rows, vocab, token, prob, arg, stream
+    "fdl_softmax_confidence": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _p, _p]),
     "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),
     "fdl_validate_work": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i64]),
     "fdl_validate_vblocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i32]),

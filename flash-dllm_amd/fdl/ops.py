@@ -242,3 +242,23 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
     _lib.call("fdl_silu_mul", gate.data_ptr(), up.data_ptr(), gate.numel(), out.data_ptr(),
               _stream(gate))
     return out
+
+
+def softmax_confidence(logits: torch.Tensor, token: torch.Tensor | None = None
+                       ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(prob float64 [rows], arg int64 [rows]) of bf16 logits [rows, vocab]
+    (fdl_softmax_confidence): without `token`, the float64 softmax maximum of each row and
+    the first index of its maximum (torch.max(softmax(logits.double(), -1), -1)); with
+    `token` [rows] int64, the float64 softmax probability of that token."""
+    _need(logits, "logits", BF16, 2)
+    dev = logits.device
+    n, vocab = logits.shape
+    if token is not None:
+        _need(token, "token", torch.int64, 1, dev)
+        if token.shape[0] != n:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "token must have one entry per row")
+    prob = torch.empty(n, dtype=torch.float64, device=dev)
+    arg = torch.empty(n, dtype=torch.int64, device=dev)
+    _lib.call("fdl_softmax_confidence", logits.data_ptr(), n, vocab, _ptr(token),
+              prob.data_ptr(), arg.data_ptr(), _stream(logits))
+    return prob, arg

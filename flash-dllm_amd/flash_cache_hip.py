@@ -123,6 +123,16 @@ def _adjacent_gate_up(block) -> torch.Tensor | None:
     return torch.as_strided(wg, (2 * h, d), (d, 1))
 
 
+def _ff_out_residual(block, x: torch.Tensor, og_x: torch.Tensor) -> torch.Tensor:
+    """og_x + dropout(ff_out(x)) (flash_cache_triton.py:634-636); with an identity dropout
+    and no bias the residual add rides in the GEMM (beta = 1), saving a pass over the rows."""
+    w = block.ff_out.weight
+    if (_identity_dropout(block.dropout) and getattr(block.ff_out, "bias", None) is None
+            and x.dim() == 2 and og_x.dim() == 2 and x.dtype == og_x.dtype == w.dtype):
+        return torch.addmm(og_x, x, w.t())
+    return og_x + block.dropout(block.ff_out(x))
+
+
 def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
     """attn_out + residual + SiLU-gated MLP + residual (flash_cache_triton.py:618-638)."""
     att = self.attn_out(att)
@@ -144,19 +154,14 @@ def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
         h = self.ff_proj.weight.shape[0]
         gu = F.linear(x, w_gu)
         x = ops.silu_mul(gu[:, :h], gu[:, h:])
-        x = self.ff_out(x)
-        x = self.dropout(x)
-        return (og_x + x).unsqueeze(0)
+        return _ff_out_residual(self, x, og_x).unsqueeze(0)
     x, x_up = self.ff_proj(x), self.up_proj(x)
     if ck is None and isinstance(self.act, torch.nn.SiLU) and x.dtype == torch.bfloat16:
         x = ops.silu_mul(x, x_up)
     else:
         x = ck(self.act, x) if ck is not None else self.act(x)
         x = x * x_up
-    x = self.ff_out(x)
-    x = self.dropout(x)
-    x = og_x + x
-    return x.unsqueeze(0)
+    return _ff_out_residual(self, x, og_x).unsqueeze(0)
 
 
 def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengths,

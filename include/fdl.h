@@ -201,6 +201,19 @@ int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* out, void* s
 int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_rows, int64_t width,
                       int64_t ld, void* out, void* stream);
 
+/*
+ * LM-head confidence. Replaces, for bf16 logits rows [n_rows][vocab] (contiguous, 16-byte
+ * aligned, vocab a multiple of 8):
+ *   token == NULL: p = softmax(logits.to(float64), -1); prob, arg = max(p, -1)
+ *                  (generate.py:218, :320): prob[r] = the float64 softmax maximum of row r,
+ *                  arg[r] (if arg != NULL) = the first index of the row's maximum logit;
+ *   token != NULL: prob[r] = softmax(logits[r].to(float64))[token[r]] (generate.py:337),
+ *                  0 for a token outside [0, vocab); arg[r] as above if arg != NULL.
+ * The float64 terms are the same as torch's; the order of the float64 sum differs.
+ */
+int fdl_softmax_confidence(const void* logits, int64_t n_rows, int64_t vocab,
+                           const int64_t* token, double* prob, int64_t* arg, void* stream);
+
 /* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
  * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
 int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,

@@ -68,6 +68,9 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 16, 8, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_silu_mul_rows", None, None, 4, 16, 32, None, None)
     lib.call("fdl_silu_mul_rows", None, None, 0, 16, 32, None, None)  # zero rows: no-op
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_softmax_confidence", None, 4, 12, None, None, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_softmax_confidence", None, 4, 16, None, None, None, None)
+    lib.call("fdl_softmax_confidence", None, 0, 16, None, None, None, None)  # zero rows: no-op
 
 
 def test_gate_up_weights_share_one_buffer():
