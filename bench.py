@@ -226,7 +226,7 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
         table[b, :pages[b]] = perm[nxt:nxt + pages[b]]
         nxt += pages[b]
     n_slots = n_pages * P
-    seqs, row, slot_list = [], 0, []
+    seqs, row, slot_list, logical_list = [], 0, [], []
     for b in range(NB):
         k = int(k_ends[b])
         logical = np.arange(k) if full[b] else None
@@ -236,6 +236,7 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
             f = int(rng.integers(96, k - 32 + 1))
             rest = rng.choice(f, qn - m, replace=False) if qn > m else np.zeros(0, np.int64)
             logical = np.concatenate([np.arange(f, f + m), rest])
+        logical_list.append(logical)
         slot_list.append(table[b, logical // P].astype(np.int64) * P + logical % P)
         qn = len(logical)
         seqs.append(SeqRows(batch=b, k_end=k, rows=np.arange(row, row + qn), n_imp=min(qn, 32)))
@@ -249,8 +250,8 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
     ang = np.concatenate([ang, ang], 1)
     sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
     cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
-    rope_row = torch.from_numpy(np.concatenate(
-        [np.arange(len(s)) if full[b] else (s % P) for b, s in enumerate(slot_list)]).astype(np.int64)).to(dev)
+    # RoPE at each row's logical position in its sequence
+    rope_row = torch.from_numpy(np.concatenate(logical_list).astype(np.int64)).to(dev)
     kc = bf(n_slots, D)
     vc = bf(n_slots, D)
     q = torch.empty((Q, D), dtype=torch.bfloat16, device=dev)
