@@ -338,6 +338,77 @@ def test_block_attention_softmax_importance_store_and_two_pass():
     _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
 
 
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT])
+def test_block_attention_key_ranges_beyond_the_staged_slot_map(imp_mode):
+    """Key ranges longer than the 2048 keys whose slots a workgroup stages in LDS (slots then
+    come straight from the page table, raw importance is stored directly): a 2500-key
+    sequence with 40 rows (64-row tile), one with 100 rows (128-row tile), and a 300-row
+    recompute over 3000 keys (256-row tiles), permuted 32-slot pages."""
+    rng = np.random.default_rng(13)
+    B, H, P = 3, 4, 32
+    k_ends = [2500, 2200, 3000]
+    n_q = [40, 100, 300]
+    max_pages = 3000 // P + 1
+    n_pages = sum((k + P - 1) // P for k in k_ends) + 5
+    perm = rng.permutation(n_pages)
+    table = np.zeros((B, max_pages), np.int32)
+    nxt = 0
+    for b in range(B):
+        n = (k_ends[b] + P - 1) // P
+        table[b, :n] = perm[nxt:nxt + n]
+        nxt += n
+    seqs, q0 = [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
+                            n_imp=32 if imp_mode else 0))
+        q0 += n_q[b]
+    Q = q0
+    q, kc, vc = _attn_inputs(14, Q, n_pages * P, H)
+    plan = make_plan(seqs, table, 5, device=DEV)
+    plan.validate(Q, n_pages * P)
+    assert plan.n_long == 2 and plan.n_mid == 1 and plan.n_work == 4
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, n_pages * P), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(n_pages * P, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode,
+                        imp if imp_mode else None)
+    if imp_mode:
+        ops.importance_accumulate(imp, plan, 1.0, scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    got = _np(out)
+    sc = scores.cpu().numpy()
+    for sq in seqs:
+        keys = orc.key_slots(sq.batch, sq.k_end, 0, table, P)
+        ref = orc.attend(qn[sq.rows], kn[keys], vn[keys], H, scale)
+        _close(got[sq.rows], ref, what=f"seq {sq.batch} ({sq.k_end} keys, {len(sq.rows)} rows)")
+        if imp_mode:
+            exp = kn[keys] @ qn[sq.rows[:sq.n_imp]].astype(np.float64).sum(0)
+            _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"importance seq {sq.batch}")
+
+
+def test_verify_attention_key_list_beyond_the_staged_slot_map():
+    """Verify blocks whose cache-key lists exceed 2048 entries (3000-slot caches)."""
+    H, bm, n_blk, L = 4, 32, 3, 3000
+    key_pos, vblocks, mask, _ = _verify_case(15, n_blk, L, H, bm)
+    assert np.all(vblocks[:, 1] - vblocks[:, 0] > 2048)
+    rows = 2 * bm
+    gen = torch.Generator().manual_seed(16)
+    D = H * 128
+    q, k1, v1 = (_bf16((n_blk * rows, D), gen) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen) for _ in range(2))
+    out = torch.full((n_blk * rows, D), POISON, dtype=torch.bfloat16, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.verify_attention(q.to(DEV), k1.to(DEV), v1.to(DEV), kc.to(DEV), vc.to(DEV),
+                         torch.from_numpy(key_pos).to(DEV), torch.from_numpy(vblocks).to(DEV),
+                         torch.from_numpy(mask).to(DEV), rows, out, H, scale)
+    torch.cuda.synchronize()
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, rows, H, scale)
+    _close(_np(out), ref, what="verify attention, long key lists")
+
+
 def test_block_attention_leaves_other_rows_untouched():
     B, L, H = 2, 128, 2
     seqs = [SeqRows(0, 100, np.array([5, 1, 9])), SeqRows(1, 128, np.array([0, 7]))]
