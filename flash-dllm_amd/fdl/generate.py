@@ -182,7 +182,41 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         blk.v_cache = torch.empty((L * B, d_model), dtype=model.dtype, device=dev)
     page_table = contiguous_page_table(B, L)
     empty_i32 = torch.zeros(0, dtype=torch.int32, device=dev)
-    full_pos_d = torch.empty(B * L, dtype=torch.int64, device=dev)
+    # Device ranking (use_gpu_rank): the ranked segment of sequence j is full_pos[j, :n_j],
+    # with n_j the decoded count before the step's last acceptance stage (the pass-1 count
+    # with Flash-Verify, the pre-step count without). Both that segment and attn_scores are
+    # final once that stage is known, so the rank kernel is enqueued then, through pinned
+    # buffers, and read back after the synchronization that follows anyway (the verify
+    # probabilities, or the pass-1 confidences).
+    gpu_rank = use_gpu_rank
+    if gpu_rank:
+        if torch.device(dev).type != "cuda":
+            raise ValueError("use_gpu_rank ranks on the GPU; the model is on " + str(dev))
+        full_pos_d = torch.empty(B * L, dtype=torch.int64, device=dev)
+        fp_up = torch.empty(B * L, dtype=torch.int64, pin_memory=True)
+        fp_back = torch.empty(B * L, dtype=torch.int64, pin_memory=True)
+        seg_up = torch.empty((B, 2), dtype=torch.int32, pin_memory=True)
+        seg_d = torch.empty((B, 2), dtype=torch.int32, device=dev)
+        rank_done = torch.cuda.Event()
+    rank_len = [0] * B
+
+    def enqueue_rank() -> None:
+        """Ranks full_pos[j, :seqs[j].nd] of every active sequence on the device."""
+        act = [j for j in range(B) if active[j] != -1]
+        if not act:
+            return
+        rank_done.synchronize()  # the previous step's copies through fp_up / fp_back are done
+        fp_up.numpy()[:] = full_pos.reshape(-1)
+        seg = seg_up.numpy()
+        for i, j in enumerate(act):
+            seg[i] = (j * L, seqs[j].nd)
+            rank_len[j] = seqs[j].nd
+        full_pos_d.copy_(fp_up, non_blocking=True)
+        seg_d[:len(act)].copy_(seg_up[:len(act)], non_blocking=True)
+        ops.importance_rank(attn_scores, full_pos_d, seg_d[:len(act)],
+                            int(seg[:len(act), 1].max()))
+        fp_back.copy_(full_pos_d, non_blocking=True)
+        rank_done.record()
 
     while True:
         t_step = time.perf_counter()
@@ -229,6 +263,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             x0_p_all, x0_all = ops.softmax_confidence(logits.contiguous())
         else:
             x0_p_all, x0_all = torch.max(F.softmax(logits.to(torch.float64), dim=-1), dim=-1)
+        if gpu_rank and not verify:
+            enqueue_rank()
         x0_p_all = x0_p_all.cpu().numpy()
         x0_all = x0_all.cpu().numpy()
         del logits
@@ -292,6 +328,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 verify_meta[j] = (acc_q, T, S)
                 acc_q += len(s.verify_pos)
                 acc_k += len(keys)
+            if gpu_rank:
+                enqueue_rank()
             vq = np.concatenate([seqs[j].verify_pos for j in range(B) if active[j] != -1])
             vblocks_d = _to_dev(np.asarray(vblocks, np.int32), dev)
             key_pos_d = _to_dev(np.concatenate(key_pos).astype(np.int64), dev)
@@ -404,13 +442,14 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     s.tracked = np.zeros(0, np.int64)
                     s.verify_pos = np.zeros(0, np.int64)
         if cont:
-            segs = np.array([[j * L, seqs[j].nd - keep_num[j]] for j in cont], dtype=np.int32)
-            if use_gpu_rank:
-                full_pos_d.copy_(torch.from_numpy(full_pos.reshape(-1)), non_blocking=False)
-                ops.importance_rank(attn_scores, full_pos_d, _to_dev(segs, dev), int(segs[:, 1].max()))
-                fp = full_pos_d.cpu().numpy().reshape(B, L)
+            if gpu_rank:
+                rank_done.synchronize()
+                fp = fp_back.numpy().reshape(B, L)
                 for j in cont:
                     n = seqs[j].nd - keep_num[j]
+                    if n != rank_len[j]:
+                        raise RuntimeError(f"ranked {rank_len[j]} slots of sequence {j}, "
+                                           f"the refresh reads {n}")
                     full_pos[j, :n] = fp[j, :n]
             else:
                 sc = attn_scores.cpu().numpy()
