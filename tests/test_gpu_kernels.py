@@ -427,10 +427,10 @@ def test_block_attention_leaves_other_rows_untouched():
 
 # ------------------------------------------------------------------------- ranking
 
-@pytest.mark.parametrize("L", [200, 500, 896, 2000, 4000])
+@pytest.mark.parametrize("L", [50, 120, 200, 500, 896, 2000, 4000])
 def test_importance_rank_bit_exact(L):
-    """Every sort-network size (256 .. 4096 keys), ragged segments incl. 0 and 1 entries,
-    many ties and signed zeros."""
+    """Every sort-network size (64 .. 4096 keys; one key per thread up to 1024), ragged
+    segments incl. 0 and 1 entries, many ties and signed zeros."""
     rng = np.random.default_rng(9)
     B = 8
     scores = (rng.integers(-40, 40, B * L).astype(np.float32) * np.float32(0.25))
