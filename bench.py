@@ -404,10 +404,10 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0) -> dict:
               threshold=E2E["threshold"], gamma=E2E["gamma"], track_num=E2E["track_num"],
               mask_num=E2E["mask_num"], eos_id=cfg.eos_token_id, verify=E2E["verify"])
 
-    def decode(steps):
+    def decode(steps, kv_pages=None):
         st = DecodeStats()
         generate_with_Flash_dLLM(model, prompts, lengths, n, [None] * n, [0] * n, stats=st,
-                                 max_steps=steps, **kw)
+                                 max_steps=steps, kv_pages=kv_pages, **kw)
         return st
 
     decode(2)  # warm-up: library GEMM selection, allocator
@@ -416,6 +416,12 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0) -> dict:
            "steps": st.steps, "forwards": st.forwards, "wall_s": round(st.wall_s, 3),
            "ms_per_step": round(1e3 * st.wall_s / max(st.steps, 1), 3),
            "verify_accepted": st.verify_accepted}
+    # the same decode over a paged K/V pool with one fixed stride's worth of pages per row
+    stride = ((E2E["prompt"] + E2E["gen"] + E2E["block"]) // 128 + 1) * 128
+    stp = decode(max_steps, kv_pages=n * stride // 32)
+    out["paged_pool"] = {"tokens_per_s": stp.decoded / stp.wall_s, "steps": stp.steps,
+                         "ms_per_step": round(1e3 * stp.wall_s / max(stp.steps, 1), 3),
+                         "kv_pages": n * stride // 32}
     if torch_steps > 0:
         model.set_attention(flash_fused_elastic_cache_torch)
         stt = decode(torch_steps)

@@ -18,10 +18,15 @@
     track_num * block_m decoded entries plus the look-ahead window;
   * finished sequences are replaced by the next prompt (:405-427).
 
+With `kv_pages`, the K/V caches are a paged pool (fdl.schedule.PagePool) instead of the
+fixed stride: host arrays keep the logical layout (slot j*L + p), the caches, attn_scores
+and the kernels' slot arguments use pool slots through the page table, and a finished
+sequence's pages go back to the pool.
+
 What differs from the reference, on purpose:
   * bookkeeping (token ids, full_pos, per-sequence counters) lives in host numpy arrays,
-    so a step synchronises with the GPU three times (pass-1 confidences, verify
-    probabilities, importance ranking) instead of at every `.item()`;
+    so a step synchronises with the GPU twice (pass-1 confidences, verify probabilities;
+    the importance ranking is read back after one of them) instead of at every `.item()`;
   * the logits are computed only for the rows the step reads (the masked rows, the verify
     mask-view rows); the LM head is row-wise, so the values are the same;
   * the importance ranking runs on the GPU (fdl_importance_rank) with ties broken toward
@@ -43,7 +48,8 @@ import torch
 import torch.nn.functional as F
 
 from . import ops
-from .schedule import SeqRows, contiguous_page_table, make_plan
+from .schedule import (DEFAULT_PAGE_LOG2, PagePool, SeqRows, contiguous_page_table, make_plan,
+                       page_slots)
 
 
 def get_rotary_embedding(seq_len: int, dim: int, rope_theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -93,6 +99,12 @@ class _Seq:
     __slots__ = ("prompt", "nd", "seqlen_k", "masked", "tracked", "predicted_length",
                  "decoded_eos", "keep_rows", "verify_pos")
 
+    def __init__(self):
+        # an idle row: no prompt, no rows
+        self.prompt, self.nd, self.seqlen_k, self.predicted_length = -1, 0, 0, 0
+        self.decoded_eos, self.keep_rows = -1, 0
+        self.masked = self.tracked = self.verify_pos = np.zeros(0, np.int64)
+
 
 def _to_dev(a: np.ndarray, device, dtype=None) -> torch.Tensor:
     t = torch.from_numpy(np.ascontiguousarray(a))
@@ -119,13 +131,24 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                              mask_id=126336, threshold=0.9, gamma=0.9, track_num=4, mask_num=4, eos_id=126081,
                              verify=False, sliding_window=True, is_instruct=True, tokenizer=None,
                              stop_tokens=None, stats: DecodeStats | None = None, use_gpu_rank: bool = True,
-                             rows_only: bool = True, max_steps: int | None = None):
+                             rows_only: bool = True, max_steps: int | None = None,
+                             kv_pages: int | None = None):
     """Returns (responses, num_tokens, max_num_tokens) like llada/generate.py:472.
 
     use_gpu_rank: rank the decoded slots with fdl_importance_rank (else numpy, same order).
     rows_only: run the LM head only on the rows the step reads (else on every row).
     max_steps: stop after this many denoising steps (benchmarking a bounded sample;
         stats.decoded then counts the tokens decoded so far).
+    kv_pages: K/V caches as a pool of this many 32-slot pages (None: the fixed stride of L
+        slots per sequence). A sequence starts with the pages of its seqlen_k key slots and
+        gets more when its masked block reaches past them; admission reserves pages up to
+        max(seqlen_k, prompt + gen + block_m - 1) positions, the reach of a decode that
+        does not accept tokens past prompt + gen ahead of earlier ones (beyond the
+        reservation a sequence grows from the free pages, MemoryError if there are none).
+        A finished sequence's pages return to the pool; prompts are admitted in order into
+        idle rows while their reservation fits (MemoryError if a prompt does not fit an
+        empty pool). With pages for every row the decode is the fixed-stride decode, token
+        for token.
     """
     dev = model.device
     cfg = model.config
@@ -142,13 +165,84 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     x = np.full(B * L, mask_id, dtype=np.int64)
     x_draft = np.full(B * L, mask_id, dtype=np.int64)
     full_pos = np.arange(B * L, dtype=np.int64).reshape(B, L)
-    attn_scores = torch.zeros(B * L, dtype=torch.float32, device=dev)
+    paged = kv_pages is not None
+    PL = DEFAULT_PAGE_LOG2
+    if paged:
+        pool = PagePool(kv_pages, PL)
+        page_table = np.zeros((B, L >> PL), dtype=np.int32)
+        n_slots = pool.n_slots
+        logical_of = np.full(n_slots, -1, dtype=np.int64)  # pool slot -> j * L + p
+        seq_pages = [np.zeros(0, np.int32) for _ in range(B)]
+        reserved = [0] * B  # pages promised to row j beyond the ones it holds
+    else:
+        page_table = contiguous_page_table(B, L)
+        n_slots = B * L
+    attn_scores = torch.zeros(n_slots, dtype=torch.float32, device=dev)
     num_tokens = 0
     max_num_tokens = 0
     active = [-1] * B
     seqs = [_Seq() for _ in range(B)]
     start_layer = [-1] * B
     count = 0
+
+    def seqlen_k_of(i: int) -> int:
+        return (int(prompt_lengths[i]) + gen_length) // bn * bn + bn
+
+    def pages_needed(i: int) -> int:
+        """Pages reserved at admission (positions a decode normally reaches)."""
+        span = max(seqlen_k_of(i), int(prompt_lengths[i]) + gen_length + bm - 1)
+        return pool.pages_for(min(L, span))
+
+    def grow(j: int, n_positions: int) -> None:
+        """Gives row j pages for logical positions 0 .. n_positions - 1."""
+        have = seq_pages[j].size
+        need = pool.pages_for(n_positions)
+        if need <= have:
+            return
+        extra = pool.alloc(need - have, above=int(seq_pages[j].max()) if have else -1)
+        reserved[j] = max(0, reserved[j] - extra.size)
+        page_table[j, have:need] = extra
+        seq_pages[j] = np.concatenate([seq_pages[j], extra])
+        logical_of[page_slots(extra, extra.size << PL, PL)] = \
+            j * L + (have << PL) + np.arange(extra.size << PL)
+
+    def phys(a: np.ndarray) -> np.ndarray:
+        """Cache slots of logical slots j * L + p."""
+        if not paged:
+            return a
+        j, p = np.divmod(a, L)
+        return (page_table[j, p >> PL].astype(np.int64) << PL) | (p & ((1 << PL) - 1))
+
+    def idle(j: int) -> None:
+        s = seqs[j]
+        active[j] = -1
+        s.masked = np.zeros(0, np.int64)
+        s.tracked = np.zeros(0, np.int64)
+        s.verify_pos = np.zeros(0, np.int64)
+
+    def release(j: int) -> None:
+        if paged:
+            reserved[j] = 0
+            if seq_pages[j].size:
+                logical_of[page_slots(seq_pages[j], seq_pages[j].size << PL, PL)] = -1
+                pool.free(seq_pages[j])
+                seq_pages[j] = np.zeros(0, np.int32)
+
+    def admit(j: int) -> bool:
+        """Loads the next prompt into row j if there is one and its pages fit."""
+        nonlocal count
+        if count >= len(prompts):
+            return False
+        if paged:
+            need = pages_needed(count)
+            if pool.n_free - sum(reserved) < need:
+                return False
+            page_table[j] = 0
+            reserved[j] = need
+            grow(j, seqlen_k_of(count))
+        load_prompt(j, count)
+        count += 1
+        return True
 
     def load_prompt(j: int, i: int) -> None:
         pl = int(prompt_lengths[i])
@@ -172,15 +266,14 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         start_layer[j] = -1
 
     for j in range(B):
-        load_prompt(j, count)
-        count += 1
+        if not admit(j):
+            idle(j)
 
     sin, cos = get_rotary_embedding(L, d_model // n_heads, cfg.rope_theta, dev)
     rope = [sin.repeat(B, 1).contiguous(), cos.repeat(B, 1).contiguous()]
     for blk in model.model.transformer.blocks:
-        blk.k_cache = torch.empty((L * B, d_model), dtype=model.dtype, device=dev)
-        blk.v_cache = torch.empty((L * B, d_model), dtype=model.dtype, device=dev)
-    page_table = contiguous_page_table(B, L)
+        blk.k_cache = torch.empty((n_slots, d_model), dtype=model.dtype, device=dev)
+        blk.v_cache = torch.empty((n_slots, d_model), dtype=model.dtype, device=dev)
     empty_i32 = torch.zeros(0, dtype=torch.int32, device=dev)
     # Device ranking (use_gpu_rank): the ranked segment of sequence j is full_pos[j, :n_j],
     # with n_j the decoded count before the step's last acceptance stage (the pass-1 count
@@ -206,7 +299,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         if not act:
             return
         rank_done.synchronize()  # the previous step's copies through fp_up / fp_back are done
-        fp_up.numpy()[:] = full_pos.reshape(-1)
+        fp_up.numpy()[:] = phys(full_pos.reshape(-1))
         seg = seg_up.numpy()
         for i, j in enumerate(act):
             seg[i] = (j * L, seqs[j].nd)
@@ -220,6 +313,24 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
 
     while True:
         t_step = time.perf_counter()
+        if paged:
+            for j in range(B):
+                if active[j] == -1 and not admit(j):
+                    break
+        if all(a == -1 for a in active):
+            if count >= len(prompts):
+                break
+            raise MemoryError(f"prompt {count} needs {pages_needed(count)} pages; the pool has "
+                              f"{kv_pages}")
+        if paged:
+            # pages for every position this step touches (queries and cache writes)
+            for j in range(B):
+                if active[j] != -1:
+                    s = seqs[j]
+                    hi = max(int(s.masked.max()) if len(s.masked) else -1,
+                             int(s.tracked.max()) if len(s.tracked) else -1)
+                    if hi >= 0:
+                        grow(j, hi - j * L + 1)
         # ---- pack the step's query rows: masked rows, then tracked rows (:439-467)
         masked_blocks, tracked_blocks, seq_rows = [], [], []
         acc = 0
@@ -246,6 +357,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             seq_rows.append(SeqRows(batch=j, k_end=seqs[j].seqlen_k, rows=rows,
                                     n_imp=len(r[0]) if len(seqs[j].masked) else 0))
         plan = make_plan(seq_rows, page_table, device=dev)
+        if paged:
+            plan.kv_slot = _to_dev(phys(qpos), dev)
         mb = np.concatenate(masked_blocks) if masked_blocks else np.zeros((0, 4), np.int64)
         tb = np.concatenate(tracked_blocks) if tracked_blocks else np.zeros((0, 4), np.int64)
         mb_t, tb_t = torch.from_numpy(mb), torch.from_numpy(tb)
@@ -332,7 +445,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 enqueue_rank()
             vq = np.concatenate([seqs[j].verify_pos for j in range(B) if active[j] != -1])
             vblocks_d = _to_dev(np.asarray(vblocks, np.int32), dev)
-            key_pos_d = _to_dev(np.concatenate(key_pos).astype(np.int64), dev)
+            key_pos_d = _to_dev(phys(np.concatenate(key_pos).astype(np.int64)), dev)
             mask_d = _to_dev(np.concatenate(masks), dev)
             vq_d = _to_dev(vq, dev)
             xq = _to_dev(np.concatenate(x_verify), dev)[None]
@@ -433,14 +546,9 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     responses[i] = gen_ids.tolist()
                 num_tokens += s.nd - pl
                 max_num_tokens += gen_length
-                if count < len(prompts):
-                    load_prompt(j, count)
-                    count += 1
-                else:
-                    active[j] = -1
-                    s.masked = np.zeros(0, np.int64)
-                    s.tracked = np.zeros(0, np.int64)
-                    s.verify_pos = np.zeros(0, np.int64)
+                release(j)
+                if not admit(j):
+                    idle(j)
         if cont:
             if gpu_rank:
                 rank_done.synchronize()
@@ -450,15 +558,16 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     if n != rank_len[j]:
                         raise RuntimeError(f"ranked {rank_len[j]} slots of sequence {j}, "
                                            f"the refresh reads {n}")
-                    full_pos[j, :n] = fp[j, :n]
+                    full_pos[j, :n] = logical_of[fp[j, :n]] if paged else fp[j, :n]
             else:
                 sc = attn_scores.cpu().numpy()
                 for j in cont:
                     n = seqs[j].nd - keep_num[j]
                     seg = full_pos[j, :n]
-                    v = sc[seg]
+                    ph = phys(seg)
+                    v = sc[ph]
                     v = np.where(v == 0, np.float32(0), v)
-                    full_pos[j, :n] = seg[np.lexsort((-seg, v))]
+                    full_pos[j, :n] = seg[np.lexsort((-ph, v))]
             for j in cont:
                 s = seqs[j]
                 s.masked = full_pos[j, s.nd:s.nd + bm].copy()
@@ -471,7 +580,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 start_layer[j] = n_layers
         stats.steps += 1
         stats.per_step_s.append(time.perf_counter() - t_step)
-        if all(a == -1 for a in active):
+        if all(a == -1 for a in active) and count >= len(prompts):
             break
         if max_steps is not None and stats.steps >= max_steps:
             break

@@ -44,6 +44,64 @@ def contiguous_page_table(n_seq: int, max_length: int, page_log2: int = DEFAULT_
     return (np.arange(n_seq, dtype=np.int64)[:, None] * per + np.arange(per)[None, :]).astype(np.int32)
 
 
+def page_slots(pages: np.ndarray, n: int, page_log2: int = DEFAULT_PAGE_LOG2) -> np.ndarray:
+    """Slots of logical positions 0 .. n-1 of a sequence whose page-table row is `pages`."""
+    p = np.arange(n, dtype=np.int64)
+    return (np.asarray(pages, dtype=np.int64)[p >> page_log2] << page_log2) | (p & ((1 << page_log2) - 1))
+
+
+class PagePool:
+    """Fixed pool of K/V cache pages (2^page_log2 slots each) shared by the sequences of a
+    decode. The reference gives every sequence a fixed stride of max_length slots
+    (llada/generate.py:76-79, :178-180) and refills a finished sequence's row in place
+    (:405-427); here a sequence holds only the pages its own length needs, returns them when
+    it finishes, and a new sequence is admitted when enough pages are free.
+
+    alloc() hands out the lowest free page ids in ascending order, and a sequence that grows
+    asks for ids above its last page first, so within a sequence the slot order normally
+    follows the logical position order (the importance ranking breaks score ties by slot;
+    with ascending pages it breaks them as the contiguous layout does)."""
+
+    def __init__(self, n_pages: int, page_log2: int = DEFAULT_PAGE_LOG2):
+        if n_pages < 1:
+            raise ValueError(f"a page pool needs at least one page (got {n_pages})")
+        self.n_pages = int(n_pages)
+        self.page_log2 = page_log2
+        self._free = np.ones(self.n_pages, dtype=bool)
+
+    @property
+    def page_size(self) -> int:
+        return 1 << self.page_log2
+
+    @property
+    def n_slots(self) -> int:
+        return self.n_pages << self.page_log2
+
+    @property
+    def n_free(self) -> int:
+        return int(self._free.sum())
+
+    def pages_for(self, n_positions: int) -> int:
+        return -(-int(n_positions) // self.page_size)
+
+    def alloc(self, n: int, above: int = -1) -> np.ndarray:
+        """n free pages (int32, ascending); the lowest free ids above `above` first, then the
+        lowest below it. Raises MemoryError if fewer than n are free."""
+        free = np.flatnonzero(self._free)
+        if n > free.size:
+            raise MemoryError(f"page pool: {n} pages requested, {free.size} of {self.n_pages} free")
+        free = np.concatenate([free[free > above], free[free <= above]])
+        got = free[:n]
+        self._free[got] = False
+        return got.astype(np.int32)
+
+    def free(self, pages: np.ndarray) -> None:
+        pages = np.asarray(pages, dtype=np.int64)
+        if pages.size and (self._free[pages].any() or len(np.unique(pages)) != pages.size):
+            raise ValueError("page pool: freeing a page that is not allocated")
+        self._free[pages] = True
+
+
 def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS, mid_rows: int = MID_TILE_ROWS,
                long_rows: int = LONG_TILE_ROWS) -> tuple[np.ndarray, np.ndarray, int, int]:
     """Splits each sequence's rows into tiles of three classes.
@@ -128,6 +186,9 @@ class AttnPlan:
     page_log2: int
     n_long: int = 0  # leading work items that are long (256-row) tiles
     n_mid: int = 0   # the next work items, mid (128-row) tiles
+    # K/V cache slots of the packed query rows when they differ from the query positions
+    # (a paged pool: the positions index the RoPE table, these slots the cache); device int64
+    kv_slot: torch.Tensor = field(repr=False, default=None)
     work_d: torch.Tensor = field(repr=False, default=None)
     row_idx_d: torch.Tensor = field(repr=False, default=None)
     page_table_d: torch.Tensor = field(repr=False, default=None)

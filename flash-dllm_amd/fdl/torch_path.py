@@ -15,6 +15,8 @@ import math
 import torch
 import torch.nn.functional as F
 
+from .schedule import AttnPlan, page_slots
+
 
 def _rotate(t: torch.Tensor, sin: torch.Tensor, cos: torch.Tensor, n_heads: int) -> torch.Tensor:
     """Rotate-half RoPE per head in float32 (flash_cache_triton.py:90-93, :433-441)."""
@@ -81,25 +83,33 @@ def flash_fused_elastic_cache_torch(self, x: torch.Tensor, block_idx, positions,
             allow[:, k1 - k0:] = attn_mask[vi * rows: vi * rows + nr, :nr].bool()
             att[q0:q1], _ = _attend(q[q0:q1], keys, vals, n_heads, softmax_scale, allow)
     else:
+        # a plan over a paged pool: the query rows' cache slots, and each sequence's keys
+        # through its page-table row (contiguous slots b * max_length + n otherwise)
+        paged = isinstance(info, AttnPlan) and info.kv_slot is not None
+        slot = info.kv_slot if paged else pos
         if x.shape[0] > 0:
-            self.k_cache.index_copy_(0, pos, k.to(self.k_cache.dtype))
-            self.v_cache.index_copy_(0, pos, v.to(self.v_cache.dtype))
+            self.k_cache.index_copy_(0, slot, k.to(self.k_cache.dtype))
+            self.v_cache.index_copy_(0, slot, v.to(self.v_cache.dtype))
         importance = block_idx > 1
         S_mean = None
         if importance:
-            S_mean = torch.zeros(batch_size * max_length, dtype=torch.float32, device=x.device)
+            n = self.k_cache.shape[0] if paged else batch_size * max_length
+            S_mean = torch.zeros(n, dtype=torch.float32, device=x.device)
         for table, is_masked in ((query_masked_blocks, True), (query_tracked_blocks, False)):
             if table is None or len(table) == 0:
                 continue
             for b, k_end, q0, q1 in table.tolist():
-                base = b * max_length
-                out, raw = _attend(q[q0:q1], self.k_cache[base: base + k_end],
-                                   self.v_cache[base: base + k_end], n_heads, softmax_scale,
-                                   want_logits=importance and is_masked)
+                if paged:
+                    keys = torch.from_numpy(page_slots(info.page_table[b], k_end,
+                                                       info.page_log2)).to(x.device)
+                else:
+                    keys = torch.arange(b * max_length, b * max_length + k_end, device=x.device)
+                out, raw = _attend(q[q0:q1], self.k_cache[keys], self.v_cache[keys], n_heads,
+                                   softmax_scale, want_logits=importance and is_masked)
                 att[q0:q1] = out
                 if raw is not None:
                     # S.mean((0, 1)) over [block_m, n_heads] (flash_cache_triton.py:538, :615)
-                    S_mean[base: base + k_end] += raw.sum(dim=(0, 1)) / (block_m * n_heads)
+                    S_mean[keys] += raw.sum(dim=(0, 1)) / (block_m * n_heads)
         if importance:
             attn_scores += S_mean
 

@@ -31,7 +31,9 @@ lengths   = [start_layer, query_verify_blocks, query_masked_blocks, query_tracke
              elastic_cache, verify]
 `info` (unused by the reference kernels) may carry a precomputed fdl.schedule.AttnPlan;
 otherwise the plan is derived from the masked/tracked block tables once per forward
-(the same table objects are passed to every layer) and reused by all layers.
+(the same table objects are passed to every layer) and reused by all layers. A plan over a
+paged K/V pool carries `kv_slot`, the cache slots of the query rows; query_pos_flat then
+indexes only the RoPE tables, and key_pos_flat (verify) and attn_scores use pool slots.
 """
 from __future__ import annotations
 
@@ -198,11 +200,17 @@ def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengt
     else:
         n_rows = x.shape[0]
         if n_rows > 0:
-            ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,
-                               self.v_proj.weight, sin, cos, query_pos_flat, q, self.k_cache,
-                               self.v_cache, n_heads)
             plan = info if isinstance(info, AttnPlan) else _plan_from_tables(
                 query_masked_blocks, query_tracked_blocks, batch_size, max_length, x.device)
+            if plan.kv_slot is not None:
+                # paged pool: positions pick the RoPE rows, the plan's slots the cache rows
+                ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,
+                                   self.v_proj.weight, sin, cos, plan.kv_slot, q, self.k_cache,
+                                   self.v_cache, n_heads, rope_row=query_pos_flat)
+            else:
+                ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,
+                                   self.v_proj.weight, sin, cos, query_pos_flat, q,
+                                   self.k_cache, self.v_cache, n_heads)
             importance = block_idx > 1 and plan.has_importance
             ws = _imp_workspace(n_heads, self.k_cache.shape[0], x.device) if importance else None
             ops.block_attention(q, self.k_cache, self.v_cache, plan, att, n_heads, softmax_scale,

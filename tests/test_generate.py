@@ -131,3 +131,55 @@ def test_verify_mask_closed_form_matches_construction(T, S):
     if T + 2 * S != 2 * bm:
         T = 2 * bm - 2 * S
     np.testing.assert_array_equal(verify_mask(T, S, bm), orc.verify_mask(T, S, bm))
+
+
+def test_page_pool_alloc_free():
+    from fdl.schedule import PagePool, page_slots
+    pool = PagePool(10)
+    a = pool.alloc(3)
+    b = pool.alloc(4)
+    assert a.tolist() == [0, 1, 2] and b.tolist() == [3, 4, 5, 6] and pool.n_free == 3
+    pool.free(a)
+    c = pool.alloc(5)  # lowest free ids, ascending
+    assert c.tolist() == [0, 1, 2, 7, 8] and pool.n_free == 1
+    with pytest.raises(MemoryError):
+        pool.alloc(2)
+    with pytest.raises(ValueError):
+        pool.free(np.array([9]))  # never allocated
+    pool.free(b)
+    with pytest.raises(ValueError):
+        pool.free(b)  # twice
+    assert pool.pages_for(33) == 2 and pool.n_slots == 320
+    s = page_slots(np.array([7, 2]), 40)
+    assert s[:32].tolist() == list(range(224, 256)) and s[32:].tolist() == list(range(64, 72))
+
+
+@pytest.mark.parametrize("eos", [509, 511])
+@pytest.mark.parametrize("verify", [False, True])
+def test_paged_pool_decode_matches_fixed_stride(verify, eos):
+    """The decode over a paged K/V pool (pages handed out per sequence, grown, returned and
+    reused on refill) gives the fixed-stride decode token for token when every row fits;
+    with a pool too small for all rows at once, prompts wait for pages and still decode to
+    the same tokens (each sequence's decode depends only on its own rows).
+    Fixed stride: L = ((96 + 48 + 16) // 128 + 1) * 128 = 256 slots = 8 pages per row.
+    Reservations max(seqlen_k, prompt + 48 + 15): 4, 8, 5, 8, 4 pages; prompt 79 starts with
+    the 4 pages of its 128 keys. With EOS 511, which this model rarely emits, sequences
+    decode past prompt + gen (as the reference loop does) and grow page by page beyond
+    their reservation, up to the 8 pages of the stride."""
+    model = _model(1.0, seed=6)
+    lengths = [64, 96, 79, 80, 64]
+    prompts = _prompts(5, lengths, TINY["vocab_size"], seed=8)
+    kw = dict(gen_length=48, block_length=16, mask_id=510, threshold=0.9, gamma=0.9,
+              track_num=1, mask_num=1, eos_id=eos, verify=verify, use_gpu_rank=False,
+              rows_only=False)
+    st = [0] * 5
+    r0, n0, m0 = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, st, **kw)
+    for pages, full in ((24, True),) + (((12, False),) if eos == 509 else ()):
+        stp = [0] * 5
+        r1, n1, m1 = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, stp,
+                                              kv_pages=pages, **kw)
+        assert r1 == r0 and n1 == n0 and m1 == m0, pages
+        if full:
+            assert stp == st
+    with pytest.raises(MemoryError):
+        generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, [0] * 5, kv_pages=7, **kw)

@@ -201,3 +201,25 @@ def test_device_rank_matches_host_rank(verify):
                                            stats=st, use_gpu_rank=gpu, **kw)
         out.append((r, n, st.steps, st.forwards))
     assert out[0] == out[1]
+
+
+@pytest.mark.parametrize("verify", [False, True])
+def test_paged_pool_decode_matches_fixed_stride_on_gpu(verify):
+    """The HIP decode over a paged K/V pool (page-table attention, K/V written at pool slots
+    with RoPE rows at the logical positions, verify keys and importance at pool slots,
+    device ranking mapped back) gives the fixed-stride decode token for token. Prompt 79
+    grows a page when its masked block passes its 128 keys."""
+    model = _model(lm_head_std=1.0, seed=3)
+    rng = np.random.default_rng(11)
+    lengths = [96, 128, 79, 72, 80]
+    prompts = [torch.from_numpy(rng.integers(0, 2000, n)) for n in lengths]
+    kw = dict(gen_length=96, block_length=32, mask_id=2046, threshold=0.9, gamma=0.9,
+              track_num=1, mask_num=1, eos_id=2045, verify=verify)
+    L = orc.max_length_for([max(lengths)], 96, 32)
+    out = []
+    for pages in (None, 3 * L // 32):
+        st = DecodeStats()
+        r, n, m = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, [0] * 5,
+                                           stats=st, kv_pages=pages, **kw)
+        out.append((r, n, m, st.steps, st.forwards))
+    assert out[0] == out[1]
