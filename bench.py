@@ -9,8 +9,10 @@ slots), 512 rows in all; d_model 4096, 32 heads x 128, RoPE theta 5e5.
     2. block-table attention, masked and tracked rows of a sequence in one tile, with
        attention-importance = column sums of softmax(QK^T/sqrt(128)) over the masked
        rows                                                  (fdl_block_attention)
-    3. head reduction of the importance into the scores      (fdl_importance_accumulate)
-    4. top-32 of the decoded slots by importance             (fdl_importance_rank)
+    3. the step's ranking, as at a step's last layer: the layer's head reduction of the
+       importance into the scores of every key, then the top-32 of the decoded slots, in
+       one launch                                            (fdl_importance_accumulate_rank)
+       (at the other layers, step 3 is the head reduction alone, fdl_importance_accumulate)
 
     python bench.py [--steps K] [--warmup W] [--no-cpu]
 
@@ -83,6 +85,8 @@ def build_workload(seed: int, device):
         dev["plan"].validate(Q, B * L)
         full_pos = np.arange(B * L, dtype=np.int64).reshape(B, L)
         dev["full_pos"] = torch.from_numpy(full_pos).to(device)
+        dev["seg_keys"] = torch.from_numpy(np.array([[b, K_END] for b in range(B)],
+                                                    dtype=np.int32)).to(device)
         dev["seg"] = torch.from_numpy(np.array([[b * L, int(f)] for b, f in enumerate(frontier)],
                                                dtype=np.int32)).to(device)
     return host, dev
@@ -140,7 +144,7 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     plan = d["plan"]
     scale = 1.0 / np.sqrt(HD)
     max_len = int(host["frontier"].max())
-    names = ["qkv_rope_cache", "block_attention", "importance_accumulate", "importance_rank"]
+    names = ["qkv_rope_cache", "block_attention", "importance_accumulate_rank"]
 
     def step(ev=None):
         def mark(i):
@@ -152,10 +156,10 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
         mark(1)
         ops.block_attention(q, kc, vc, plan, att, H, scale, lib.IMP_SOFTMAX_COLSUM, imp)
         mark(2)
-        ops.importance_accumulate(imp, plan, 1.0, scores)
+        # the step's last layer: its head reduction folded into the top-32 ranking
+        ops.importance_rank(scores, d["full_pos"], d["seg"], max_len, topk, TOPK, imp_part=imp,
+                            scale=1.0, plan=plan, seg_keys=d["seg_keys"])
         mark(3)
-        ops.importance_rank(scores, d["full_pos"], d["seg"], max_len, topk, TOPK)
-        mark(4)
 
     for _ in range(warmup):
         step()
@@ -170,7 +174,8 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
     # pass 2: per-kernel durations from events around every launch
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+           for _ in range(steps)]
     for i in range(steps):
         step(evs[i])
     torch.cuda.synchronize()
@@ -479,8 +484,7 @@ def main() -> int:
         "block_attention": {"us": t_attn, "TFLOP/s": attn_f / t_attn / 1e6,
                             "GB/s": attn_b / t_attn / 1e3,
                             "hbm_frac": attn_b / t_attn / 1e3 / PEAK_HBM_GBS},
-        "importance_accumulate": {"us": per["importance_accumulate"]},
-        "importance_rank": {"us": per["importance_rank"]},
+        "importance_accumulate_rank": {"us": per["importance_accumulate_rank"]},
     }
     achieved = qkv_f / t_qkv / 1e6
     traffic = measured_traffic()

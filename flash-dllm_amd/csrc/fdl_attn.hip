@@ -1169,7 +1169,8 @@ __global__ __launch_bounds__(256) void imp_accumulate_kernel(
       for (int u = 0; u < 8; ++u) sum += v[u];
     }
     for (; hh < n_heads; ++hh) sum += part[int64_t(hh) * n_slots + s];
-    scores[s] += scale * sum;
+    // one fma, as fdl_importance_accumulate_rank does for the step's last layer
+    scores[s] = __builtin_fmaf(scale, sum, scores[s]);
   }
 }
 

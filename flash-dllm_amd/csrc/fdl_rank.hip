@@ -16,6 +16,12 @@
 // lanes 1 and 2 apart, ds_swizzle for 4, 8 and 16, a lane permute for 32), and only the
 // strides of 64R and above go through LDS with a workgroup barrier (10 of the 55 steps for
 // 1024 keys with 1024 threads of one key).
+//
+// rank_kernel<T, R, true> (fdl_importance_accumulate_rank) first does, for the sequence
+// of its segment, what fdl_importance_accumulate does for that sequence's keys (page-table
+// order, so the per-head loads are coalesced; heads summed in ascending order, then one fma
+// into the score), then, after a workgroup barrier, ranks the segment by the new scores:
+// the step's last head reduction and its ranking in one launch.
 #include "fdl_device.h"
 #include "fdl_host.h"
 
@@ -115,20 +121,77 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&key)[R], int tid, uint64
   if constexpr (K < T * R) bitonic_sort<T, R, 2 * K>(key, tid, xbuf, buf);
 }
 
-template <int T, int R>
-__global__ __launch_bounds__(T) void rank_kernel(const float* __restrict__ scores,
-                                                 int64_t n_scores, int64_t* slots,
-                                                 int64_t n_slot_entries,
-                                                 const int32_t* __restrict__ seg, int max_len,
-                                                 int64_t* topk_out, int k) {
+struct RankArgs {
+  float* scores;  // read; written only by the accumulating variant
+  int64_t n_scores;
+  int64_t* slots;
+  int64_t n_slot_entries;
+  const int32_t* seg;
+  int max_len;
+  int64_t* topk_out;
+  int k;
+  // accumulating variant only
+  const float* part;  // [n_heads][n_scores]
+  int n_heads;
+  float scale;
+  const int32_t* page_table;  // [n_seq][max_pages]
+  int n_seq;
+  int max_pages;
+  int page_log2;
+  const int32_t* seg_keys;  // [n_seg][2]: page-table row, key count of the segment's sequence
+};
+
+// The head sum of fdl_importance_accumulate for one slot: ascending head order, loads
+// issued 16 at a time.
+__device__ __forceinline__ float head_sum(const float* __restrict__ part, int n_heads,
+                                          int64_t n_scores, int64_t slot) {
+  float sum = 0.f;
+  int h = 0;
+  for (; h + 16 <= n_heads; h += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = part[int64_t(h + u) * n_scores + slot];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) sum += v[u];
+  }
+  for (; h < n_heads; ++h) sum += part[int64_t(h) * n_scores + slot];
+  return sum;
+}
+
+template <int T, int R, bool kAcc>
+__global__ __launch_bounds__(T) void rank_kernel(RankArgs a) {
   constexpr int P = T * R;
+  float* __restrict__ scores = a.scores;
+  const int64_t n_scores = a.n_scores;
+  int64_t* slots = a.slots;
+  const int64_t n_slot_entries = a.n_slot_entries;
+  const int32_t* __restrict__ seg = a.seg;
+  const int max_len = a.max_len;
+  int64_t* topk_out = a.topk_out;
+  const int k = a.k;
+  const int tid = threadIdx.x;
+
+  if constexpr (kAcc) {
+    const int b = a.seg_keys[2 * blockIdx.x], k_end = a.seg_keys[2 * blockIdx.x + 1];
+    // a row or key count out of range (rejected by the host) accumulates nothing
+    if (b >= 0 && b < a.n_seq && k_end > 0 &&
+        int64_t(k_end) <= (int64_t(a.max_pages) << a.page_log2)) {
+      const int32_t* ptab = a.page_table + int64_t(b) * a.max_pages;
+      const int pmask = (1 << a.page_log2) - 1;
+      for (int n = tid; n < k_end; n += T) {
+        const int64_t sl = (int64_t(ptab[n >> a.page_log2]) << a.page_log2) | (n & pmask);
+        if (sl < 0 || sl >= n_scores) continue;
+        scores[sl] = __builtin_fmaf(a.scale, head_sum(a.part, a.n_heads, n_scores, sl), scores[sl]);
+      }
+    }
+    __syncthreads();  // the segment's entries read the scores stored above
+  }
   __shared__ uint64_t xbuf[2][P];
   const int s = blockIdx.x;
   const int64_t start = seg[2 * s];
   int len = seg[2 * s + 1];
   // a segment longer than max_len (rejected by the host) is left as is
   if (start < 0 || len < 0 || len > max_len || len > P || start + len > n_slot_entries) len = 0;
-  const int tid = threadIdx.x;
 
   uint64_t key[R];
 #pragma unroll
@@ -164,12 +227,45 @@ __global__ __launch_bounds__(T) void rank_kernel(const float* __restrict__ score
 }
 
 template <int T, int R>
-hipError_t launch_rank(int64_t n_seg, hipStream_t st, const float* scores, int64_t n_scores,
-                       int64_t* slots, int64_t n_slot_entries, const int32_t* seg, int max_len,
-                       int64_t* topk_out, int k) {
-  hipLaunchKernelGGL((rank_kernel<T, R>), dim3(static_cast<unsigned>(n_seg)), dim3(T), 0, st,
-                     scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
+hipError_t launch_rank(int64_t n_seg, hipStream_t st, const RankArgs& a) {
+  if (a.part)
+    hipLaunchKernelGGL((rank_kernel<T, R, true>), dim3(static_cast<unsigned>(n_seg)), dim3(T),
+                       0, st, a);
+  else
+    hipLaunchKernelGGL((rank_kernel<T, R, false>), dim3(static_cast<unsigned>(n_seg)), dim3(T),
+                       0, st, a);
   return hipGetLastError();
+}
+
+// Shared by both entry points: checks, then the launch shape by segment length.
+int rank_entry(const char* fn, RankArgs a, int64_t n_seg, void* stream) {
+  FDL_REQUIRE(n_seg >= 0 && n_seg < (int64_t(1) << 31), FDL_ERR_SHAPE,
+              "%s: n_seg = %lld out of range", fn, (long long)n_seg);
+  if (n_seg == 0) return ok();
+  FDL_REQUIRE(a.scores && a.slots && a.seg, FDL_ERR_NULL, "%s: scores/slots/seg is NULL", fn);
+  FDL_REQUIRE(a.max_len >= 0 && a.max_len <= kMaxLen, FDL_ERR_UNSUPPORTED,
+              "%s: max_len = %d outside [0, %d]", fn, a.max_len, kMaxLen);
+  FDL_REQUIRE(a.n_scores >= 1 && a.n_scores <= 0x7fffffff, FDL_ERR_SHAPE,
+              "%s: n_scores = %lld outside [1, 2^31)", fn, (long long)a.n_scores);
+  FDL_REQUIRE(a.k >= 0, FDL_ERR_SHAPE, "%s: k = %d < 0", fn, a.k);
+  FDL_REQUIRE(a.topk_out != nullptr || a.k == 0, FDL_ERR_NULL,
+              "%s: topk_out is NULL with k = %d", fn, a.k);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int m = a.max_len;
+  hipError_t e;
+  // One key per thread up to 1024 keys (threads rounded up to a power of two), then 2, 4 and
+  // 8 keys per thread of 1024 threads. The segment is latency-bound: at 768 keys one key
+  // per thread takes 6.5 us against 7.5 us at four keys per thread (measured on MI355X).
+  if (m <= 64) e = launch_rank<64, 1>(n_seg, st, a);
+  else if (m <= 128) e = launch_rank<128, 1>(n_seg, st, a);
+  else if (m <= 256) e = launch_rank<256, 1>(n_seg, st, a);
+  else if (m <= 512) e = launch_rank<512, 1>(n_seg, st, a);
+  else if (m <= 1024) e = launch_rank<1024, 1>(n_seg, st, a);
+  else if (m <= 2048) e = launch_rank<1024, 2>(n_seg, st, a);
+  else if (m <= 4096) e = launch_rank<1024, 4>(n_seg, st, a);
+  else e = launch_rank<1024, 8>(n_seg, st, a);
+  FDL_HIP_CHECK(e);
+  return ok();
 }
 
 }  // namespace
@@ -179,41 +275,30 @@ extern "C" int fdl_importance_rank(const float* scores, int64_t n_scores, int64_
                                    int64_t n_slot_entries, const int32_t* seg, int64_t n_seg,
                                    int32_t max_len, int64_t* topk_out, int32_t k,
                                    void* stream) {
+  fdl::RankArgs a{const_cast<float*>(scores), n_scores, slots, n_slot_entries, seg, max_len,
+                  topk_out, k, nullptr, 0, 0.f, nullptr, 0, 0, 0, nullptr};
+  return fdl::rank_entry("fdl_importance_rank", a, n_seg, stream);
+}
+
+extern "C" int fdl_importance_accumulate_rank(
+    const float* imp_part, int64_t n_heads, float scale, const int32_t* page_table,
+    int64_t n_seq, int64_t max_pages, int32_t page_log2, const int32_t* seg_keys, float* scores,
+    int64_t n_scores, int64_t* slots, int64_t n_slot_entries, const int32_t* seg, int64_t n_seg,
+    int32_t max_len, int64_t* topk_out, int32_t k, void* stream) {
   using namespace fdl;
-  FDL_REQUIRE(n_seg >= 0 && n_seg < (int64_t(1) << 31), FDL_ERR_SHAPE,
-              "fdl_importance_rank: n_seg = %lld out of range", (long long)n_seg);
-  if (n_seg == 0) return ok();
-  FDL_REQUIRE_PTR(scores);
-  FDL_REQUIRE_PTR(slots);
-  FDL_REQUIRE_PTR(seg);
-  FDL_REQUIRE(max_len >= 0 && max_len <= kMaxLen, FDL_ERR_UNSUPPORTED,
-              "fdl_importance_rank: max_len = %d outside [0, %d]", max_len, kMaxLen);
-  FDL_REQUIRE(n_scores >= 1 && n_scores <= 0x7fffffff, FDL_ERR_SHAPE,
-              "fdl_importance_rank: n_scores = %lld outside [1, 2^31)", (long long)n_scores);
-  FDL_REQUIRE(k >= 0, FDL_ERR_SHAPE, "fdl_importance_rank: k = %d < 0", k);
-  FDL_REQUIRE(topk_out != nullptr || k == 0, FDL_ERR_NULL,
-              "fdl_importance_rank: topk_out is NULL with k = %d", k);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  // One key per thread up to 1024 keys (threads rounded up to a power of two), then 2, 4 and
-  // 8 keys per thread of 1024 threads. The segment is latency-bound: at 768 keys one key
-  // per thread takes 6.5 us against 7.5 us at four keys per thread (measured on MI355X).
-  if (max_len <= 64)
-    e = launch_rank<64, 1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 128)
-    e = launch_rank<128, 1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 256)
-    e = launch_rank<256, 1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 512)
-    e = launch_rank<512, 1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 1024)
-    e = launch_rank<1024, 1>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 2048)
-    e = launch_rank<1024, 2>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else if (max_len <= 4096)
-    e = launch_rank<1024, 4>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  else
-    e = launch_rank<1024, 8>(n_seg, st, scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k);
-  FDL_HIP_CHECK(e);
-  return ok();
+  FDL_REQUIRE(n_heads >= 1 && n_heads <= 65535, FDL_ERR_SHAPE,
+              "fdl_importance_accumulate_rank: n_heads = %lld outside [1, 65535]",
+              (long long)n_heads);
+  FDL_REQUIRE(n_seq >= 1 && n_seq < (int64_t(1) << 31) && max_pages >= 1 &&
+                  max_pages < (int64_t(1) << 31),
+              FDL_ERR_SHAPE, "fdl_importance_accumulate_rank: page table [%lld][%lld] out of range",
+              (long long)n_seq, (long long)max_pages);
+  FDL_REQUIRE(page_log2 >= 0 && page_log2 <= 16, FDL_ERR_SHAPE,
+              "fdl_importance_accumulate_rank: page_log2 = %d outside [0, 16]", page_log2);
+  FDL_REQUIRE(n_seg <= 0 || (imp_part && page_table && seg_keys), FDL_ERR_NULL,
+              "fdl_importance_accumulate_rank: imp_part/page_table/seg_keys is NULL");
+  RankArgs a{scores, n_scores, slots, n_slot_entries, seg, max_len, topk_out, k, imp_part,
+             static_cast<int>(n_heads), scale, page_table, static_cast<int>(n_seq),
+             static_cast<int>(max_pages), page_log2, seg_keys};
+  return rank_entry("fdl_importance_accumulate_rank", a, n_seg, stream);
 }

@@ -91,6 +91,8 @@ class DecodeStats:
     rows: int = 0
     verify_accepted: int = 0  # tokens accepted by the verify pass
     decoded: int = 0          # tokens decoded (both passes), finished or not
+    fused_rank_steps: int = 0  # steps whose ranking folded in the last layer's reduction
+    split_rank_steps: int = 0  # steps that reduced first (a ranked row without importance)
     wall_s: float = 0.0
     per_step_s: list = field(default_factory=list)
 
@@ -288,8 +290,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         full_pos_d = torch.empty(B * L, dtype=torch.int64, device=dev)
         fp_up = torch.empty(B * L, dtype=torch.int64, pin_memory=True)
         fp_back = torch.empty(B * L, dtype=torch.int64, pin_memory=True)
-        seg_up = torch.empty((B, 2), dtype=torch.int32, pin_memory=True)
-        seg_d = torch.empty((B, 2), dtype=torch.int32, device=dev)
+        seg_up = torch.empty((2, B, 2), dtype=torch.int32, pin_memory=True)
+        seg_d = torch.empty((2, B, 2), dtype=torch.int32, device=dev)
         rank_done = torch.cuda.Event()
     rank_len = [0] * B
 
@@ -300,14 +302,26 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             return
         rank_done.synchronize()  # the previous step's copies through fp_up / fp_back are done
         fp_up.numpy()[:] = phys(full_pos.reshape(-1))
-        seg = seg_up.numpy()
+        seg = seg_up.numpy()  # [0]: (start, len) of each segment, [1]: (row, seqlen_k)
         for i, j in enumerate(act):
-            seg[i] = (j * L, seqs[j].nd)
+            seg[0, i] = (j * L, seqs[j].nd)
+            seg[1, i] = (j, seqs[j].seqlen_k)
             rank_len[j] = seqs[j].nd
         full_pos_d.copy_(fp_up, non_blocking=True)
-        seg_d[:len(act)].copy_(seg_up[:len(act)], non_blocking=True)
-        ops.importance_rank(attn_scores, full_pos_d, seg_d[:len(act)],
-                            int(seg[:len(act), 1].max()))
+        seg_d.copy_(seg_up, non_blocking=True)
+        # The last layer's head reduction, when the driver deferred it, rides in the ranking:
+        # it covers the keys [0, seqlen_k) of the ranked rows, which are the rows with
+        # importance rows (every active row has a masked block); otherwise it runs first.
+        part, scale = plan.deferred_importance or (None, 1.0)
+        if part is not None and not all(j in imp_rows for j in act):
+            ops.importance_accumulate(part, plan, scale, attn_scores)
+            part = None
+            stats.split_rank_steps += 1
+        elif part is not None:
+            stats.fused_rank_steps += 1
+        n = len(act)
+        ops.importance_rank(attn_scores, full_pos_d, seg_d[0, :n], int(seg[0, :n, 1].max()),
+                            imp_part=part, scale=scale, plan=plan, seg_keys=seg_d[1, :n])
         fp_back.copy_(full_pos_d, non_blocking=True)
         rank_done.record()
 
@@ -357,6 +371,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             seq_rows.append(SeqRows(batch=j, k_end=seqs[j].seqlen_k, rows=rows,
                                     n_imp=len(r[0]) if len(seqs[j].masked) else 0))
         plan = make_plan(seq_rows, page_table, device=dev)
+        plan.defer_last_importance = gpu_rank
+        imp_rows = {sr.batch for sr in seq_rows if sr.n_imp > 0}
         if paged:
             plan.kv_slot = _to_dev(phys(qpos), dev)
         mb = np.concatenate(masked_blocks) if masked_blocks else np.zeros((0, 4), np.int64)

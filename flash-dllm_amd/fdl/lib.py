@@ -81,6 +81,13 @@ SIGNATURES: dict[str, tuple] = {
         _p, _i64, _i32,               # seg, n_seg, max_len
         _p, _i32, _p,                 # topk_out, k, stream
     ]),
+    "fdl_importance_accumulate_rank": (ctypes.c_int, [
+        _p, _i64, _f32,               # imp_part, n_heads, scale
+        _p, _i64, _i64, _i32, _p,     # page_table, n_seq, max_pages, page_log2, seg_keys
+        _p, _i64, _p, _i64,           # scores, n_scores, slots, n_slot_entries
+        _p, _i64, _i32,               # seg, n_seg, max_len
+        _p, _i32, _p,                 # topk_out, k, stream
+    ]),
     "fdl_verify_attention": (ctypes.c_int, [
         _p, _p, _p, _p, _p,           # q, k_blk, v_blk, k_cache, v_cache
         _i64, _i64, _i64, _i64, _i64,  # n_q_rows, n_slots, d_model, n_heads, head_dim

@@ -141,10 +141,26 @@ def importance_accumulate(imp_part: torch.Tensor, plan: AttnPlan, scale: float,
 
 
 def importance_rank(scores: torch.Tensor, slots: torch.Tensor, seg: torch.Tensor, max_len: int,
-                    topk_out: torch.Tensor | None = None, k: int = 0) -> None:
+                    topk_out: torch.Tensor | None = None, k: int = 0,
+                    imp_part: torch.Tensor | None = None, scale: float = 1.0,
+                    plan: AttnPlan | None = None, seg_keys: torch.Tensor | None = None) -> None:
     """Sorts each segment (start, len) of `slots` in place by importance and gathers the
-    top-k (fdl_importance_rank)."""
+    top-k (fdl_importance_rank). With `imp_part` [n_heads, n_scores], `plan` (its page
+    table) and `seg_keys` int32 [n_seg, 2] = (page-table row, key count) per segment, first
+    reduces imp_part into the scores of each segment's sequence keys, as
+    importance_accumulate does (fdl_importance_accumulate_rank)."""
     dev = scores.device
+    if imp_part is not None:
+        _need(imp_part, "imp_part", torch.float32, 2, dev)
+        if imp_part.shape[1] != scores.shape[0]:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "imp_part must be [n_heads, len(scores)]")
+        if plan is None or seg_keys is None:
+            raise _lib.FdlError(_lib.FDL_ERR_NULL, "imp_part needs plan and seg_keys")
+        _need(seg_keys, "seg_keys", torch.int32, 2, dev)
+        if tuple(seg_keys.shape) != (seg.shape[0], 2):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "seg_keys must be [n_seg, 2]")
+        if plan.page_table_d is None:
+            plan.to(dev)
     _need(scores, "scores", torch.float32, 1)
     _need(slots, "slots", torch.int64, None, dev)
     _need(seg, "seg", torch.int32, 2, dev)
@@ -154,9 +170,18 @@ def importance_rank(scores: torch.Tensor, slots: torch.Tensor, seg: torch.Tensor
         _need(topk_out, "topk_out", torch.int64, 2, dev)
         if tuple(topk_out.shape) != (seg.shape[0], k):
             raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "topk_out must be [n_seg, k]")
+    kk = int(k if topk_out is not None else 0)
+    if imp_part is not None:
+        _lib.call("fdl_importance_accumulate_rank", imp_part.data_ptr(), imp_part.shape[0],
+                  float(scale), plan.page_table_d.data_ptr(), plan.page_table.shape[0],
+                  plan.page_table.shape[1], plan.page_log2, seg_keys.data_ptr(),
+                  scores.data_ptr(), scores.shape[0], slots.data_ptr(),
+                  slots.numel(), seg.data_ptr(), seg.shape[0], int(max_len), _ptr(topk_out), kk,
+                  _stream(scores))
+        return
     _lib.call("fdl_importance_rank", scores.data_ptr(), scores.shape[0], slots.data_ptr(),
-              slots.numel(), seg.data_ptr(), seg.shape[0], int(max_len), _ptr(topk_out),
-              int(k if topk_out is not None else 0), _stream(scores))
+              slots.numel(), seg.data_ptr(), seg.shape[0], int(max_len), _ptr(topk_out), kk,
+              _stream(scores))
 
 
 def verify_attention(q: torch.Tensor, k_blk: torch.Tensor, v_blk: torch.Tensor,

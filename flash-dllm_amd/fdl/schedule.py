@@ -189,6 +189,11 @@ class AttnPlan:
     # K/V cache slots of the packed query rows when they differ from the query positions
     # (a paged pool: the positions index the RoPE table, these slots the cache); device int64
     kv_slot: torch.Tensor = field(repr=False, default=None)
+    # The caller ranks after the forward with fdl_importance_accumulate_rank: the last layer
+    # leaves its per-head importance in deferred_importance = (imp_part, scale) instead of
+    # reducing it into attn_scores.
+    defer_last_importance: bool = False
+    deferred_importance: tuple = field(repr=False, default=None)
     work_d: torch.Tensor = field(repr=False, default=None)
     row_idx_d: torch.Tensor = field(repr=False, default=None)
     page_table_d: torch.Tensor = field(repr=False, default=None)

@@ -217,6 +217,10 @@ def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengt
                                 _lib.IMP_RAW_LOGIT if importance else _lib.IMP_NONE, ws)
             if importance:
                 # S.mean((0, 1)) divides by block_m * n_heads (flash_cache_triton.py:538, :615)
-                ops.importance_accumulate(ws, plan, 1.0 / (block_m * n_heads), attn_scores)
+                scale = 1.0 / (block_m * n_heads)
+                if plan.defer_last_importance and block_idx == self.config.n_layers - 1:
+                    plan.deferred_importance = (ws, scale)  # reduced by the caller's ranking
+                else:
+                    ops.importance_accumulate(ws, plan, scale, attn_scores)
 
     return block_mlp_tail(self, x, att)

@@ -147,6 +147,27 @@ int fdl_importance_rank(const float* scores, int64_t n_scores, int64_t* slots,
                         int32_t max_len, int64_t* topk_out, int32_t k, void* stream);
 
 /*
+ * The step's last head reduction fused into the ranking. Segment i belongs to the sequence
+ * in page-table row seg_keys[i][0], whose keys are n in [0, seg_keys[i][1]); for each of
+ * those keys (slot = slot(row, n) in [0, n_scores))
+ *   scores[slot] = fma(scale, sum_{h = 0..n_heads-1} imp_part[h][slot], scores[slot])
+ * (heads summed in ascending order: bit for bit what fdl_importance_accumulate stores for
+ * a tile of that sequence with keys [0, k_end)), then the segment is ranked and its top-k
+ * gathered as by fdl_importance_rank. Replaces, at a step's last layer,
+ * `attn_scores += S.mean((0, 1))` (flash_cache_triton.py:614-615) followed by the sort of
+ * generate.py:364-366 and the gather of :375-381. Segment entries that are not keys of
+ * their sequence keep their score. A page-table row may appear in at most one segment.
+ *   imp_part fp32 [n_heads][n_scores] (fdl_block_attention's per-head importance)
+ *   seg_keys int32 [n_seg][2]
+ */
+int fdl_importance_accumulate_rank(const float* imp_part, int64_t n_heads, float scale,
+                                   const int32_t* page_table, int64_t n_seq, int64_t max_pages,
+                                   int32_t page_log2, const int32_t* seg_keys, float* scores,
+                                   int64_t n_scores, int64_t* slots, int64_t n_slot_entries,
+                                   const int32_t* seg, int64_t n_seg, int32_t max_len,
+                                   int64_t* topk_out, int32_t k, void* stream);
+
+/*
  * Flash-Verify attention. Replaces _flash_verify_attention_fwd (flash_cache_triton.py:
  * 341-428, launched at :523-535): for each verify block (k0, k1, q0, q1) and head, the
  * rows [q0, q1) attend to the cache keys key_slots[k0..k1) and to the block's own rows

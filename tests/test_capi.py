@@ -59,6 +59,13 @@ def test_launchers_reject_bad_scalars_without_gpu():
     lib.call("fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128, None, 1, 1, 5, None,
              0, None, 1, 64, 0.1, None, 0, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_rank", None, 10, None, 10, None, 1, 16, None, 0, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 5,
+            None, None, 10, None, 10, None, 1, 16, None, 0, None)
+    assert lib.load().fdl_last_error().decode().startswith("fdl_importance_accumulate_rank")
+    _expect(lib.FDL_ERR_SHAPE, "fdl_importance_accumulate_rank", None, 0, 1.0, None, 1, 4, 5,
+            None, None, 10, None, 10, None, 1, 16, None, 0, None)
+    _expect(lib.FDL_ERR_SHAPE, "fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 17,
+            None, None, 10, None, 10, None, 1, 16, None, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32,
             128, None, 0, None, 1, None, 64, 0.1, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 1,

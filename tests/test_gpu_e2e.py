@@ -185,22 +185,31 @@ def test_greedy_decode_agreement_teacher_forced(verify):
 @pytest.mark.parametrize("verify", [False, True])
 def test_device_rank_matches_host_rank(verify):
     """The device ranking (enqueued where its inputs are final, read back after the step's
-    next synchronization) and the host ranking (numpy lexsort with the same tie rule) give
-    identical decodes: same tokens, same step and forward counts. The kernels are
-    deterministic (no atomics), so any difference is a ranking difference."""
-    model = _model(lm_head_std=1.0, seed=2)
-    rng = np.random.default_rng(9)
-    lengths = [96, 128, 100, 72, 80]
-    prompts = [torch.from_numpy(rng.integers(0, 2000, n)) for n in lengths]
-    kw = dict(gen_length=96, block_length=32, mask_id=2046, threshold=0.9, gamma=0.9,
-              track_num=1, mask_num=1, eos_id=2045, verify=verify)
-    out = []
-    for gpu in (True, False):
-        st = DecodeStats()
-        r, n, _ = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, [0] * 5,
-                                           stats=st, use_gpu_rank=gpu, **kw)
-        out.append((r, n, st.steps, st.forwards))
-    assert out[0] == out[1]
+    next synchronization, with the last layer's head reduction folded into it) and the host
+    ranking (every layer reduced, numpy lexsort with the same tie rule) give identical
+    decodes: same tokens, same step and forward counts. The kernels are deterministic (no
+    atomics), so any difference is a ranking difference. The second model's sequences
+    accept EOS-region tokens past their keys (ranked slots that are not keys keep their
+    score)."""
+    fused = split = 0
+    for seed, rseed, lengths in ((2, 9, [96, 128, 100, 72, 80]), (3, 11, [96, 128, 79, 72, 80])):
+        model = _model(lm_head_std=1.0, seed=seed)
+        rng = np.random.default_rng(rseed)
+        prompts = [torch.from_numpy(rng.integers(0, 2000, n)) for n in lengths]
+        kw = dict(gen_length=96, block_length=32, mask_id=2046, threshold=0.9, gamma=0.9,
+                  track_num=1, mask_num=1, eos_id=2045, verify=verify)
+        out = []
+        for gpu in (True, False):
+            st = DecodeStats()
+            r, n, _ = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, [0] * 5,
+                                               stats=st, use_gpu_rank=gpu, **kw)
+            out.append((r, n, st.steps, st.forwards))
+            if gpu:
+                fused += st.fused_rank_steps
+                split += st.split_rank_steps
+        assert out[0] == out[1], seed
+    print(f"device ranking: {fused} steps fused, {split} reduced first")
+    assert fused > 0
 
 
 @pytest.mark.parametrize("verify", [False, True])

@@ -469,6 +469,60 @@ def test_importance_rank_max_segment():
     np.testing.assert_array_equal(topk_d[0].cpu().numpy(), orc.topk(scores, slots, 64))
 
 
+@pytest.mark.parametrize("L,H", [(704, 32), (3008, 20)])
+def test_importance_accumulate_rank_matches_separate_kernels(L, H):
+    """fdl_importance_accumulate_rank = fdl_importance_accumulate over each segment's
+    sequence keys followed by fdl_importance_rank, bit for bit (every score, order, top-k):
+    one key per thread (704) and four (3008), 32 heads and 20 (a partial batch of head
+    loads), permuted pages, segments longer and shorter than the key count (entries past
+    the keys keep their score), a sequence with no segment (its keys untouched)."""
+    from fdl.schedule import SeqRows, make_plan
+    rng = np.random.default_rng(12)
+    B, k, P = 6, 32, 32
+    n_pages = B * L // P
+    table = rng.permutation(n_pages).astype(np.int32).reshape(B, L // P)
+    n = n_pages * P
+    part = torch.from_numpy(rng.standard_normal((H, n)).astype(np.float32)).to(DEV)
+    base = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(DEV)
+    k_end = [int(v) for v in rng.integers(1, L + 1, B)]
+    lens = [int(v) for v in rng.integers(1, L + 1, B)]
+    k_end[0], lens[0] = L, L
+    k_end[1], lens[1] = L // 2, L  # ranked entries past the keys
+    ranked_rows = [0, 1, 2, 3, 5]  # row 4 has no segment
+    slots_of = [((table[b].astype(np.int64)[np.arange(L) // P] * P) + np.arange(L) % P)
+                for b in range(B)]
+    full_pos = np.full((B, L), -7, dtype=np.int64)
+    for b in range(B):
+        full_pos[b] = slots_of[b][rng.permutation(L)]
+        full_pos[b, :lens[b]] = slots_of[b][rng.permutation(lens[b])]
+    seg = torch.from_numpy(np.array([[b * L, lens[b]] for b in ranked_rows], np.int32)).to(DEV)
+    seg_keys = torch.from_numpy(np.array([[b, k_end[b]] for b in ranked_rows], np.int32)).to(DEV)
+    scale = 1.0 / (32 * H)
+    plan = make_plan([SeqRows(batch=b, k_end=k_end[b], rows=np.array([i]), n_imp=1)
+                      for i, b in enumerate(ranked_rows)], table, device=DEV)
+    sa, pa = base.clone(), torch.from_numpy(full_pos.copy()).to(DEV)
+    ta = torch.zeros((len(ranked_rows), k), dtype=torch.int64, device=DEV)
+    ops.importance_accumulate(part, plan, scale, sa)
+    ops.importance_rank(sa, pa, seg, max(lens), ta, k)
+    sb, pb = base.clone(), torch.from_numpy(full_pos.copy()).to(DEV)
+    tb = torch.zeros_like(ta)
+    ops.importance_rank(sb, pb, seg, max(lens), tb, k, imp_part=part, scale=scale, plan=plan,
+                        seg_keys=seg_keys)
+    torch.cuda.synchronize()
+    assert torch.equal(sb, sa) and torch.equal(pb, pa) and torch.equal(tb, ta)
+    # against float64 sums and the oracle's order of the stored scores
+    keys = np.concatenate([slots_of[b][:k_end[b]] for b in ranked_rows])
+    exp = base.cpu().double().numpy()
+    exp[keys] += scale * part.cpu().double().numpy()[:, keys].sum(0)
+    got = sb.cpu().numpy()
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6)
+    other = np.setdiff1d(np.arange(n), keys)
+    np.testing.assert_array_equal(got[other], base.cpu().numpy()[other])
+    pn = pb.cpu().numpy()
+    for b in ranked_rows:
+        np.testing.assert_array_equal(pn[b, :lens[b]], orc.rank_ascending(got, full_pos[b, :lens[b]]))
+
+
 # -------------------------------------------------------------------------- verify
 
 def _verify_case(seed, n_blk, k_cache_len, H, bm=32):
