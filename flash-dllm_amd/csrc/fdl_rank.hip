@@ -142,11 +142,19 @@ struct RankArgs {
 };
 
 // The head sum of fdl_importance_accumulate for one slot: ascending head order, loads
-// issued 16 at a time.
+// issued 16 at a time (32 at once for 32 heads).
 __device__ __forceinline__ float head_sum(const float* __restrict__ part, int n_heads,
                                           int64_t n_scores, int64_t slot) {
   float sum = 0.f;
   int h = 0;
+  if (n_heads == 32) {
+    float v[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) v[u] = part[int64_t(u) * n_scores + slot];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) sum += v[u];
+    return sum;
+  }
   for (; h + 16 <= n_heads; h += 16) {
     float v[16];
 #pragma unroll
@@ -171,6 +179,20 @@ __global__ __launch_bounds__(T) void rank_kernel(RankArgs a) {
   const int k = a.k;
   const int tid = threadIdx.x;
 
+  __shared__ uint64_t xbuf[2][P];
+  const int s = blockIdx.x;
+  const int64_t start = seg[2 * s];
+  int len = seg[2 * s + 1];
+  // a segment longer than max_len (rejected by the host) is left as is
+  if (start < 0 || len < 0 || len > max_len || len > P || start + len > n_slot_entries) len = 0;
+  // the segment's slots (their loads overlap the reduction below)
+  int64_t slot_r[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid * R + r;
+    slot_r[r] = i < len ? slots[start + i] : -1;
+  }
+
   if constexpr (kAcc) {
     const int b = a.seg_keys[2 * blockIdx.x], k_end = a.seg_keys[2 * blockIdx.x + 1];
     // a row or key count out of range (rejected by the host) accumulates nothing
@@ -186,20 +208,13 @@ __global__ __launch_bounds__(T) void rank_kernel(RankArgs a) {
     }
     __syncthreads();  // the segment's entries read the scores stored above
   }
-  __shared__ uint64_t xbuf[2][P];
-  const int s = blockIdx.x;
-  const int64_t start = seg[2 * s];
-  int len = seg[2 * s + 1];
-  // a segment longer than max_len (rejected by the host) is left as is
-  if (start < 0 || len < 0 || len > max_len || len > P || start + len > n_slot_entries) len = 0;
-
   uint64_t key[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = tid * R + r;
     uint64_t kv = ~uint64_t(0);
     if (i < len) {
-      const int64_t slot = slots[start + i];
+      const int64_t slot = slot_r[r];
       // an out-of-range slot (rejected by the host) ranks below every real score
       const float sc = (slot >= 0 && slot < n_scores) ? scores[slot] : -INFINITY;
       kv = (uint64_t(orderable(sc)) << 32) | uint64_t(0xffffffffu - uint32_t(slot));
