@@ -20,7 +20,10 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """torch's current stream on t's device, as the raw handle the C ABI takes (the same
+    value as torch.cuda.current_stream(t.device).cuda_stream, without building the Python
+    stream object on every launch)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = None,

@@ -127,11 +127,14 @@ def _adjacent_gate_up(block) -> torch.Tensor | None:
 
 def _ff_out_residual(block, x: torch.Tensor, og_x: torch.Tensor) -> torch.Tensor:
     """og_x + dropout(ff_out(x)) (flash_cache_triton.py:634-636); with an identity dropout
-    and no bias the residual add rides in the GEMM (beta = 1), saving a pass over the rows."""
+    and no bias the residual add rides in the GEMM (beta = 1) and the GEMM accumulates into
+    og_x in place (og_x is the block's own residual-stream tensor), saving a pass over the
+    rows and a copy."""
     w = block.ff_out.weight
     if (_identity_dropout(block.dropout) and getattr(block.ff_out, "bias", None) is None
-            and x.dim() == 2 and og_x.dim() == 2 and x.dtype == og_x.dtype == w.dtype):
-        return torch.addmm(og_x, x, w.t())
+            and x.dim() == 2 and og_x.dim() == 2 and x.dtype == og_x.dtype == w.dtype
+            and og_x.is_contiguous()):
+        return og_x.addmm_(x, w.t())
     return og_x + block.dropout(block.ff_out(x))
 
 
