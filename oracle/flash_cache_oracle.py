@@ -22,11 +22,15 @@ How each function is pinned (tests/test_oracle_*.py):
   block_attention      torch scaled_dot_product_attention; one-key/equal-key
                        closed forms                                          (pinned)
   importance_raw_S     (sum_r q_r) . k_n closed form per head                (pinned)
+  importance_accumulate  S.mean((0, 1)) of that closed form, same test       (pinned)
   importance_softmax   explicit softmax-matrix column sums                   (pinned)
   verify_attention     torch SDPA with a boolean mask over gathered keys     (pinned)
   verify_mask          hand-worked matrices for (T, S) = (2, 3), (0, 2)      (pinned)
   rank_ascending/topk  brute force with Python sorted() on (score, slot)     (pinned)
   make_blocks          hand-worked tables                                    (pinned)
+  key_slots            paged == contiguous attention over the same keys      (pinned)
+  max_length_for, seqlen_k_for, softmax_scale
+                       hand-worked values of the reference's formulas        (pinned)
 """
 from __future__ import annotations
 
