@@ -64,7 +64,7 @@ def _qkv_case(seed, n_heads, Q, n_slots, slots, kv_packed=False, theta=500000.0,
     return q_out, kc, vc, q_ref, k_ref, v_ref, slot.numpy()
 
 
-def test_qkv_rope_cache_cfg1_shape():
+def test_qkv_rope_cache_40_rows_one_sequence():
     """40 query rows (32-token masked block + 8 tracked slots), d_model 4096, 32 heads,
     theta 5e5, cache of 512 slots: Q/K/V within tolerance, untouched slots bit-exact."""
     rng = np.random.default_rng(1)
@@ -77,7 +77,7 @@ def test_qkv_rope_cache_cfg1_shape():
     assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
 
 
-def test_qkv_rope_cache_cfg2_shape():
+def test_qkv_rope_cache_512_rows_batch8():
     """512 rows over 8 sequences of a 896-slot stride (32 masked + 32 tracked each)."""
     rng = np.random.default_rng(2)
     B, L = 8, 896
@@ -173,7 +173,7 @@ def _attn_inputs(seed, Q, n_slots, n_heads):
 
 
 @pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM])
-def test_block_attention_cfg2_shape(imp_mode):
+def test_block_attention_batch8_cache768(imp_mode):
     """8 sequences, k_end 768 of a 896 stride, 32 masked + 32 tracked rows each, 32 heads;
     masked and tracked rows share one tile per sequence."""
     rng = np.random.default_rng(4)
@@ -550,7 +550,7 @@ def _verify_case(seed, n_blk, k_cache_len, H, bm=32):
             np.concatenate(masks), np.concatenate(qslots).astype(np.int64))
 
 
-def test_verify_attention_cfg4_shape():
+def test_verify_attention_batch16_cache1024():
     """16 verify blocks over 1024-slot caches, S in [4, 16] candidates (2S draft/mask rows)
     plus fill rows, 32 heads; own-draft masking from the reference's mask construction."""
     H, bm, n_blk, L = 32, 32, 16, 1024
