@@ -117,6 +117,26 @@ def _to_dev(a: np.ndarray, device, dtype=None) -> torch.Tensor:
     return t.to(device)
 
 
+def _to_dev_many(arrays: list, device) -> list:
+    """Uploads several host arrays through one pinned buffer and one copy (16-byte aligned
+    slices; dtypes and shapes kept). The step's table uploads sit between two GPU
+    synchronisations, so each separate copy is GPU idle time."""
+    arrays = [np.ascontiguousarray(a) for a in arrays]
+    if torch.device(device).type != "cuda":
+        return [torch.from_numpy(a.copy()).to(device) for a in arrays]
+    offs, total = [], 0
+    for a in arrays:
+        offs.append(total)
+        total += (a.nbytes + 15) // 16 * 16
+    host = torch.empty(max(total, 16), dtype=torch.uint8, pin_memory=True)
+    hv = host.numpy()
+    for a, o in zip(arrays, offs):
+        hv[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+    buf = host.to(device, non_blocking=True)
+    return [buf[o:o + a.nbytes].view(torch.from_numpy(np.empty(0, a.dtype)).dtype).view(a.shape)
+            for a, o in zip(arrays, offs)]
+
+
 def _accepts_logit_rows(model) -> bool:
     """True if model.forward takes a `logit_rows` argument (this build's model does; the
     reference's LLaDAModelLM does not)."""
@@ -373,13 +393,14 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
         plan = make_plan(seq_rows, page_table, device=dev)
         plan.defer_last_importance = gpu_rank
         imp_rows = {sr.batch for sr in seq_rows if sr.n_imp > 0}
-        if paged:
-            plan.kv_slot = _to_dev(phys(qpos), dev)
         mb = np.concatenate(masked_blocks) if masked_blocks else np.zeros((0, 4), np.int64)
         tb = np.concatenate(tracked_blocks) if tracked_blocks else np.zeros((0, 4), np.int64)
         mb_t, tb_t = torch.from_numpy(mb), torch.from_numpy(tb)
-        qpos_d = _to_dev(qpos, dev)
-        x_query = _to_dev(x[qpos], dev)[None]
+        if paged:
+            qpos_d, x_query, plan.kv_slot = _to_dev_many([qpos, x[qpos], phys(qpos)], dev)
+        else:
+            qpos_d, x_query = _to_dev_many([qpos, x[qpos]], dev)
+        x_query = x_query[None]
         positions = [qpos_d, empty_i32, rope, plan, attn_scores, []]
         lengths = [start_layer, None, mb_t, tb_t, torch.cat([mb_t, tb_t]), active, len(mb), L, bm, bn, None,
                    False]
@@ -460,24 +481,23 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             if gpu_rank:
                 enqueue_rank()
             vq = np.concatenate([seqs[j].verify_pos for j in range(B) if active[j] != -1])
-            vblocks_d = _to_dev(np.asarray(vblocks, np.int32), dev)
-            key_pos_d = _to_dev(phys(np.concatenate(key_pos).astype(np.int64)), dev)
-            mask_d = _to_dev(np.concatenate(masks), dev)
-            vq_d = _to_dev(vq, dev)
-            xq = _to_dev(np.concatenate(x_verify), dev)[None]
             # only the mask-view rows [T+S, T+2S) of each block are read (:318)
             lr = np.concatenate([np.arange(a + T + S, a + T + 2 * S) for (a, T, S) in verify_meta.values()])
+            draft_rows = np.concatenate([np.arange(a + T, a + T + S) for (a, T, S) in verify_meta.values()])
+            xv = np.concatenate(x_verify)
+            vblocks_d, key_pos_d, mask_d, vq_d, xq, lr_d, draft_tok = _to_dev_many(
+                [np.asarray(vblocks, np.int32), phys(np.concatenate(key_pos).astype(np.int64)),
+                 np.concatenate(masks), vq, xv, lr.astype(np.int64), xv[draft_rows]], dev)
+            xq = xq[None]
             positions = [vq_d, key_pos_d, rope, None, attn_scores, mask_d]
             lengths = [start_layer, vblocks_d, None, tb_t, None, active, len(mb), L, bm, bn, None, True]
             if len(lr):
                 vlog = model(xq, use_cache=True, lengths=lengths, positions=positions,
-                             **row_kw(_to_dev(lr, dev))).logits.squeeze(0)
+                             **row_kw(lr_d)).logits.squeeze(0)
                 if not rows_only:
-                    vlog = vlog[_to_dev(lr, dev)]
+                    vlog = vlog[lr_d]
                 stats.forwards += 1
                 stats.rows += len(vq)
-                draft_rows = np.concatenate([np.arange(a + T, a + T + S) for (a, T, S) in verify_meta.values()])
-                draft_tok = _to_dev(np.concatenate(x_verify)[draft_rows], dev)
                 if vlog.dtype == torch.bfloat16 and vlog.is_cuda:
                     pv = ops.softmax_confidence(vlog.contiguous(), draft_tok)[0]
                 else:
