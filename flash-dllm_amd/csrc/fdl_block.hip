@@ -104,14 +104,17 @@ __global__ __launch_bounds__(kEwThreads) void silu_mul_kernel(const uint16_t* __
   }
 }
 
-// Rows of a [gate | up] buffer: row r's gate at g + r * ld, its up at u + r * ld, its output
-// at out + r * 8 * w8 (w8 16-byte chunks per row).
+// Rows of a [gate | up] buffer: row r's gate at g + r * ld, its up at u + r * ld. The
+// output row is cut into column chunks of q8 16-byte vectors (w8 = n_chunks * q8 per row);
+// chunk q of row r goes to out + 8 * (q * n_rows * q8 + r * q8) (one chunk: plain rows).
 __global__ __launch_bounds__(kEwThreads) void silu_mul_rows_kernel(
     const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, int64_t ld, int64_t w8,
-    int64_t n8, uint16_t* __restrict__ out) {
+    int64_t q8, int64_t n_rows, int64_t n8, uint16_t* __restrict__ out) {
   for (int64_t c = int64_t(blockIdx.x) * kEwThreads + threadIdx.x; c < n8;
        c += int64_t(gridDim.x) * kEwThreads) {
     const int64_t r = c / w8, j8 = c - r * w8;
+    const int64_t q = j8 / q8;
+    const int64_t o8 = (q * n_rows + r) * q8 + (j8 - q * q8);
     const u32x4 a = ld16(g + r * ld + 8 * j8), b = ld16(u + r * ld + 8 * j8);
     u32x4 o;
 #pragma unroll
@@ -121,6 +124,42 @@ __global__ __launch_bounds__(kEwThreads) void silu_mul_rows_kernel(
       const float s1 = round_bf(g1 / (1.0f + expf(-g1)));
       o[j] = pack_bf16x2(s0 * bf_lo(b[j]), s1 * bf_hi(b[j]));
     }
+    st16(out + 8 * o8, o);
+  }
+}
+
+// out[i] = bf16(float(out[i]) + sum_s part[s][i]), the partials summed in ascending s first;
+// 8 columns (one 16-byte bf16 vector, two 16-byte fp32 vectors per partial) per step.
+__global__ __launch_bounds__(kEwThreads) void split_reduce_residual_kernel(
+    const float* __restrict__ part, int n_split, int64_t stride, int64_t n8,
+    uint16_t* __restrict__ out) {
+  for (int64_t c = int64_t(blockIdx.x) * kEwThreads + threadIdx.x; c < n8;
+       c += int64_t(gridDim.x) * kEwThreads) {
+    float acc[8];
+    {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(part + 8 * c);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(part + 8 * c + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] = a[j];
+        acc[4 + j] = b[j];
+      }
+    }
+    for (int sp = 1; sp < n_split; ++sp) {
+      const float* p = part + sp * stride + 8 * c;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] += a[j];
+        acc[4 + j] += b[j];
+      }
+    }
+    const u32x4 r = ld16(out + 8 * c);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16x2(bf_lo(r[j]) + acc[2 * j], bf_hi(r[j]) + acc[2 * j + 1]);
     st16(out + 8 * c, o);
   }
 }
@@ -189,12 +228,16 @@ extern "C" int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* o
 }
 
 extern "C" int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_rows,
-                                 int64_t width, int64_t ld, void* out, void* stream) {
+                                 int64_t width, int64_t ld, int64_t out_chunks, void* out,
+                                 void* stream) {
   using namespace fdl;
   FDL_REQUIRE(n_rows >= 0 && width >= 0 && width % 8 == 0 && ld % 8 == 0 && ld >= width,
               FDL_ERR_UNSUPPORTED,
               "fdl_silu_mul_rows: width = %lld, ld = %lld (multiples of 8, ld >= width)",
               (long long)width, (long long)ld);
+  FDL_REQUIRE(out_chunks >= 1 && width % (8 * out_chunks) == 0, FDL_ERR_UNSUPPORTED,
+              "fdl_silu_mul_rows: out_chunks = %lld must divide width / 8 = %lld",
+              (long long)out_chunks, (long long)(width / 8));
   if (n_rows == 0 || width == 0) return ok();
   FDL_REQUIRE_PTR(gate);
   FDL_REQUIRE_PTR(up);
@@ -206,7 +249,30 @@ extern "C" int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_row
   const int64_t blocks = std::min<int64_t>((n8 + kEwThreads - 1) / kEwThreads, 256 * 8);
   hipLaunchKernelGGL(silu_mul_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads),
                      0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate),
-                     static_cast<const uint16_t*>(up), ld, w8, n8, static_cast<uint16_t*>(out));
+                     static_cast<const uint16_t*>(up), ld, w8, w8 / out_chunks, n_rows, n8,
+                     static_cast<uint16_t*>(out));
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}
+
+extern "C" int fdl_split_reduce_residual(const float* part, int64_t n_split, int64_t n_rows,
+                                         int64_t n_cols, void* residual_out, void* stream) {
+  using namespace fdl;
+  FDL_REQUIRE(n_split >= 1 && n_split <= 64, FDL_ERR_UNSUPPORTED,
+              "fdl_split_reduce_residual: n_split = %lld outside [1, 64]", (long long)n_split);
+  FDL_REQUIRE(n_rows >= 0 && n_cols >= 0 && n_cols % 8 == 0, FDL_ERR_UNSUPPORTED,
+              "fdl_split_reduce_residual: n_cols = %lld (a multiple of 8 is implemented)",
+              (long long)n_cols);
+  if (n_rows == 0 || n_cols == 0) return ok();
+  FDL_REQUIRE_PTR(part);
+  FDL_REQUIRE_PTR(residual_out);
+  FDL_REQUIRE_ALIGNED(part, 16);
+  FDL_REQUIRE_ALIGNED(residual_out, 16);
+  const int64_t n = n_rows * n_cols, n8 = n / 8;
+  const int64_t blocks = std::min<int64_t>((n8 + kEwThreads - 1) / kEwThreads, 256 * 8);
+  hipLaunchKernelGGL(split_reduce_residual_kernel, dim3(static_cast<unsigned>(blocks)),
+                     dim3(kEwThreads), 0, static_cast<hipStream_t>(stream), part,
+                     static_cast<int>(n_split), n, n8, static_cast<uint16_t*>(residual_out));
   FDL_HIP_CHECK(hipGetLastError());
   return ok();
 }

@@ -101,7 +101,8 @@ SIGNATURES: dict[str, tuple] = {
     ]),
     "fdl_silu_mul": (ctypes.c_int, [_p, _p, _i64, _p, _p]),  # gate, up, n, out, stream
     # gate, up, n_rows, width, ld, out, stream
-    "fdl_silu_mul_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
+    "fdl_silu_mul_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "fdl_split_reduce_residual": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p]),
     # logits, n_rows, vocab, token, prob, arg, stream
     "fdl_softmax_confidence": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _p, _p]),
     "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),

@@ -77,6 +77,15 @@ def _share_gate_up(block: nn.Module) -> None:
     block.up_proj.weight = nn.Parameter(buf[h:], requires_grad=wu.requires_grad)
 
 
+def _transpose_ff_out(block: nn.Module) -> None:
+    """Stores ff_out.weight ([d, h]) as the transposed view of a contiguous [h, d] buffer,
+    keeping its values: K-chunks of W^T are then plain views, the right operands of a
+    split-K ff_out product."""
+    w = block.ff_out.weight
+    block.ff_out.weight = nn.Parameter(w.detach().t().contiguous().t(),
+                                       requires_grad=w.requires_grad)
+
+
 @torch.no_grad()
 def fuse_gate_up_(model: nn.Module) -> nn.Module:
     """Re-lays every block's ff_proj / up_proj weights out as one buffer (see _share_gate_up),
@@ -84,6 +93,16 @@ def fuse_gate_up_(model: nn.Module) -> nn.Module:
     for m in model.modules():
         if hasattr(m, "ff_proj") and hasattr(m, "up_proj"):
             _share_gate_up(m)
+    return model
+
+
+@torch.no_grad()
+def transpose_ff_out_(model: nn.Module) -> nn.Module:
+    """Re-lays every block's ff_out weight out transposed (see _transpose_ff_out), for
+    models whose parameters were created or loaded elsewhere."""
+    for m in model.modules():
+        if hasattr(m, "ff_proj") and hasattr(m, "ff_out"):
+            _transpose_ff_out(m)
     return model
 
 
@@ -104,6 +123,7 @@ class LLaDALlamaBlock(nn.Module):
         self.up_proj = _linear(d, h, device, dtype)
         _share_gate_up(self)
         self.ff_out = _linear(h, d, device, dtype)
+        _transpose_ff_out(self)
         self.act = nn.SiLU()
         self.dropout = nn.Identity()
         self._activation_checkpoint_fn = None
@@ -182,7 +202,8 @@ class LLaDAModelLM(nn.Module):
 @torch.no_grad()
 def random_init_(model: LLaDAModelLM, seed: int = 0) -> LLaDAModelLM:
     """N(0, init_std) for every linear and the embedding, ones for the norms, drawn on
-    the parameters' device with a seeded generator."""
+    the parameters' device with a seeded generator, in each parameter's logical element
+    order (a weight stored transposed gets the values of the plain layout)."""
     cfg = model.config
     gen = torch.Generator(device=model.device).manual_seed(seed)
     for name, p in model.named_parameters():
@@ -191,7 +212,11 @@ def random_init_(model: LLaDAModelLM, seed: int = 0) -> LLaDAModelLM:
         else:
             std = cfg.lm_head_std if (name.endswith("transformer.ff_out.weight")
                                       and cfg.lm_head_std is not None) else cfg.init_std
-            p.normal_(0.0, std, generator=gen)
+            if p.is_contiguous():
+                p.normal_(0.0, std, generator=gen)
+            else:
+                p.copy_(torch.empty(p.shape, dtype=p.dtype, device=p.device).normal_(
+                    0.0, std, generator=gen))
     return model
 
 

@@ -243,24 +243,34 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return out if residual is None else (sum_out, out)
 
 
-def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
+             out_chunks: int = 1) -> torch.Tensor:
     """bf16(bf16(silu(gate)) * up) (fdl_silu_mul). gate and up may also be [rows, width]
     views with one common row stride and unit column stride, such as the two halves of a
-    [rows, 2 * width] product (fdl_silu_mul_rows); out is then a new contiguous tensor."""
+    [rows, 2 * width] product (fdl_silu_mul_rows); out is then a new contiguous tensor,
+    [rows, width], or with out_chunks = S > 1 the column chunks [S, rows, width / S]."""
     if up.shape != gate.shape:
         raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "up shape differs from gate")
-    if (gate.dim() == 2 and not gate.is_contiguous() and gate.stride(1) == 1
+    if out_chunks != 1 and gate.dim() != 2:
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "out_chunks needs [rows, width] operands")
+    if (gate.dim() == 2 and (out_chunks != 1 or not gate.is_contiguous()) and gate.stride(1) == 1
             and up.stride() == gate.stride()):
         for t, name in ((gate, "gate"), (up, "up")):
             if t.device.type != "cuda" or t.dtype != BF16:
                 raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} must be a bf16 GPU tensor")
         if up.device != gate.device:
             raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "up is on another device than gate")
+        rows, width = gate.shape
+        if out_chunks < 1 or width % out_chunks:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"out_chunks {out_chunks} does not divide {width}")
+        shape = (rows, width) if out_chunks == 1 else (out_chunks, rows, width // out_chunks)
         if out is None:
-            out = torch.empty(gate.shape, dtype=BF16, device=gate.device)
-        _need(out, "out", BF16, 2, gate.device)
-        _lib.call("fdl_silu_mul_rows", gate.data_ptr(), up.data_ptr(), gate.shape[0],
-                  gate.shape[1], gate.stride(0), out.data_ptr(), _stream(gate))
+            out = torch.empty(shape, dtype=BF16, device=gate.device)
+        _need(out, "out", BF16, len(shape), gate.device)
+        if tuple(out.shape) != shape:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"out must be {list(shape)}")
+        _lib.call("fdl_silu_mul_rows", gate.data_ptr(), up.data_ptr(), rows, width,
+                  gate.stride(0), out_chunks, out.data_ptr(), _stream(gate))
         return out
     _need(gate, "gate", BF16)
     _need(up, "up", BF16, None, gate.device)
@@ -270,6 +280,18 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
     _lib.call("fdl_silu_mul", gate.data_ptr(), up.data_ptr(), gate.numel(), out.data_ptr(),
               _stream(gate))
     return out
+
+
+def split_reduce_residual(part: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual = bf16(residual + sum_s part[s]) in place (fdl_split_reduce_residual):
+    part fp32 [S, rows, cols], residual bf16 [rows, cols]."""
+    _need(residual, "residual", BF16, 2)
+    _need(part, "part", torch.float32, 3, residual.device)
+    if tuple(part.shape[1:]) != tuple(residual.shape):
+        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "part must be [S, rows, cols] of the residual")
+    _lib.call("fdl_split_reduce_residual", part.data_ptr(), part.shape[0], residual.shape[0],
+              residual.shape[1], residual.data_ptr(), _stream(residual))
+    return residual
 
 
 def softmax_confidence(logits: torch.Tensor, token: torch.Tensor | None = None

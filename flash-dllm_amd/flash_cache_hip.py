@@ -125,6 +125,32 @@ def _adjacent_gate_up(block) -> torch.Tensor | None:
     return torch.as_strided(wg, (2 * h, d), (d, 1))
 
 
+# ff_out (K = mlp width, N = d_model) as a split-K product at up to SPLIT_K_MAX_ROWS rows:
+# at 512 rows its N = 4096 outputs give too few tiles for the CUs; four K-chunks as one
+# batched product with float32 partials, then one pass that adds them and the residual,
+# take 57 + 7 us against 78-82 us for the single product (LLaDA-8B shape, MI355X).
+SPLIT_K = 4
+SPLIT_K_MAX_ROWS = 1024
+_BMM_FP32_OUT = hasattr(torch.ops.aten.bmm, "dtype")  # torch.bmm(..., out_dtype=float32)
+
+
+def _split_k_ff_out(block, rows: int) -> torch.Tensor | None:
+    """ff_out.weight^T as [SPLIT_K, K / SPLIT_K, N] views when the split-K product applies
+    (bf16 GPU weight stored transposed, see fdl.model.transpose_ff_out_; no bias; identity
+    dropout; 1 .. SPLIT_K_MAX_ROWS rows), else None."""
+    lin = block.ff_out
+    w = lin.weight
+    if (not _BMM_FP32_OUT or getattr(lin, "bias", None) is not None
+            or not _identity_dropout(block.dropout) or w.dtype != torch.bfloat16
+            or not w.is_cuda or w.dim() != 2 or not 0 < rows <= SPLIT_K_MAX_ROWS):
+        return None
+    n, k = w.shape
+    wt = w.t()
+    if not wt.is_contiguous() or k % (8 * SPLIT_K) or n % 8:
+        return None
+    return wt.view(SPLIT_K, k // SPLIT_K, n)
+
+
 def _ff_out_residual(block, x: torch.Tensor, og_x: torch.Tensor) -> torch.Tensor:
     """og_x + dropout(ff_out(x)) (flash_cache_triton.py:634-636); with an identity dropout
     and no bias the residual add rides in the GEMM (beta = 1) and the GEMM accumulates into
@@ -158,6 +184,13 @@ def block_mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
         # over the two halves of each output row
         h = self.ff_proj.weight.shape[0]
         gu = F.linear(x, w_gu)
+        ws = _split_k_ff_out(self, gu.shape[0])
+        if ws is not None and og_x.is_contiguous() and og_x.dtype == torch.bfloat16:
+            # SiLU(gate) * up written as the K-chunks [S, rows, K / S]; the batched product's
+            # right operands are contiguous chunks of W^T; partials + residual in one pass
+            xs = ops.silu_mul(gu[:, :h], gu[:, h:], out_chunks=ws.shape[0])
+            part = torch.bmm(xs, ws, out_dtype=torch.float32)
+            return ops.split_reduce_residual(part, og_x).unsqueeze(0)
         x = ops.silu_mul(gu[:, :h], gu[:, h:])
         return _ff_out_residual(self, x, og_x).unsqueeze(0)
     x, x_up = self.ff_proj(x), self.up_proj(x)

@@ -216,11 +216,26 @@ int fdl_silu_mul(const void* gate, const void* up, int64_t n, void* out, void* s
  * fdl_silu_mul_rows: the same over n_rows rows whose gate and up halves are strided views,
  * e.g. the two halves of one [n_rows][2 * width] product of the concatenated ff_proj / up_proj
  * weights (one GEMM instead of the two at flash_cache_triton.py:628):
- *   out[r][c] = bf16(bf16(silu(gate[r * ld + c])) * up[r * ld + c]), out contiguous [n_rows][width].
- *   width and ld multiples of 8, ld >= width; all pointers 16-byte aligned.
+ *   y[r][c] = bf16(bf16(silu(gate[r * ld + c])) * up[r * ld + c]).
+ * The output is cut into out_chunks column chunks of w = width / out_chunks columns, stored
+ * chunk after chunk: y[r][c] at out[(c / w) * n_rows * w + r * w + c % w] ([out_chunks][n_rows][w];
+ * out_chunks = 1 is plain [n_rows][width] rows). The chunked form is the K-split operand of
+ * a split-K ff_out product. width and ld multiples of 8, ld >= width, w a multiple of 8; all
+ * pointers 16-byte aligned.
  */
 int fdl_silu_mul_rows(const void* gate, const void* up, int64_t n_rows, int64_t width,
-                      int64_t ld, void* out, void* stream);
+                      int64_t ld, int64_t out_chunks, void* out, void* stream);
+
+/*
+ * fdl_split_reduce_residual: the end of a split-K ff_out product with its residual
+ * (flash_cache_triton.py:634-636, `x = og_x + ff_out(x)`):
+ *   residual_out[i] = bf16(float(residual_out[i]) + (part[0][i] + part[1][i] + ...)),
+ * one rounding, as a GEMM that accumulates into the residual (beta = 1) rounds once.
+ *   part fp32 [n_split][n_rows][n_cols]; residual_out bf16 [n_rows][n_cols], updated in place;
+ *   n_cols % 8 == 0, pointers 16-byte aligned.
+ */
+int fdl_split_reduce_residual(const float* part, int64_t n_split, int64_t n_rows,
+                              int64_t n_cols, void* residual_out, void* stream);
 
 /*
  * LM-head confidence. Replaces, for bf16 logits rows [n_rows][vocab] (contiguous, 16-byte

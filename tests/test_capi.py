@@ -71,10 +71,15 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 1,
             1.0, None, None)
     assert lib.load().fdl_last_error().decode().startswith("fdl_importance_accumulate")
-    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 12, 16, None, None)
-    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 16, 8, None, None)
-    _expect(lib.FDL_ERR_NULL, "fdl_silu_mul_rows", None, None, 4, 16, 32, None, None)
-    lib.call("fdl_silu_mul_rows", None, None, 0, 16, 32, None, None)  # zero rows: no-op
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 12, 16, 1, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 16, 8, 1, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul_rows", None, None, 4, 16, 32, 4, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_silu_mul_rows", None, None, 4, 16, 32, 2, None, None)
+    lib.call("fdl_silu_mul_rows", None, None, 0, 16, 32, 1, None, None)  # zero rows: no-op
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_split_reduce_residual", None, 0, 4, 16, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_split_reduce_residual", None, 4, 4, 12, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_split_reduce_residual", None, 4, 4, 16, None, None)
+    lib.call("fdl_split_reduce_residual", None, 4, 0, 16, None, None)  # zero rows: no-op
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_softmax_confidence", None, 4, 12, None, None, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_softmax_confidence", None, 4, 16, None, None, None, None)
     lib.call("fdl_softmax_confidence", None, 0, 16, None, None, None, None)  # zero rows: no-op

@@ -99,3 +99,63 @@ def test_block_mlp_tail_fused_gate_up_matches_two_gemms():
     torch.cuda.synchronize()
     # the GEMM library may order the reduction differently for the wider product
     torch.testing.assert_close(fused.float(), split.float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("rows,width,chunks", [(5, 64, 2), (512, 12288, 4)])
+def test_silu_mul_rows_chunked_output(rows, width, chunks):
+    """out_chunks = S writes the same values as S column chunks [S, rows, width / S]."""
+    gen = torch.Generator().manual_seed(rows)
+    gu = (2.0 * torch.randn(rows, 2 * width, generator=gen)).to(torch.bfloat16).to(DEV)
+    gate, up = gu[:, :width], gu[:, width:]
+    plain = ops.silu_mul(gate, up)
+    chunked = ops.silu_mul(gate, up, out_chunks=chunks)
+    torch.cuda.synchronize()
+    assert chunked.shape == (chunks, rows, width // chunks)
+    assert torch.equal(chunked, plain.view(rows, chunks, width // chunks).transpose(0, 1))
+
+
+@pytest.mark.parametrize("S,rows,cols", [(1, 3, 8), (4, 512, 4096), (3, 17, 72)])
+def test_split_reduce_residual_bit_exact(S, rows, cols):
+    """residual = bf16(residual + ((p0 + p1) + p2 ...)) in place, the same float32 order."""
+    gen = torch.Generator().manual_seed(S * rows + cols)
+    part = torch.randn(S, rows, cols, generator=gen).to(DEV)
+    res = torch.randn(rows, cols, generator=gen).to(torch.bfloat16).to(DEV)
+    acc = part[0].clone()
+    for s in range(1, S):
+        acc = acc + part[s]
+    ref = (res.float() + acc).to(torch.bfloat16)
+    out = ops.split_reduce_residual(part, res)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == res.data_ptr() and torch.equal(out, ref)
+
+
+def test_block_mlp_tail_split_k_ff_out_matches_single_product():
+    """The epilogue with ff_out stored transposed (split-K: chunked SiLU output, batched
+    float32-output product, partials + residual in one pass) against the same weights in
+    the plain layout (one product accumulating into the residual), and against float32."""
+    import flash_cache_hip as fch
+    from fdl.model import LLaDAConfig, LLaDALlamaBlock
+    cfg = LLaDAConfig.llada_8b()
+    cfg.d_model, cfg.n_heads, cfg.mlp_hidden_size = 512, 4, 1536
+    blk = LLaDALlamaBlock(cfg, 0, fch.flash_fused_elastic_cache, device=DEV, dtype=torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.normal_(0.0, 0.05, generator=gen)
+    x = torch.randn(96, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    att = torch.randn(96, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    assert fch._split_k_ff_out(blk, 96) is not None
+    split = fch.block_mlp_tail(blk, x, att)
+    blk.ff_out.weight = torch.nn.Parameter(blk.ff_out.weight.detach().contiguous())
+    assert fch._split_k_ff_out(blk, 96) is None
+    single = fch.block_mlp_tail(blk, x, att)
+    # float32 reference of the same epilogue from the bf16 intermediates
+    og = x + (att.float() @ blk.attn_out.weight.float().t()).to(torch.bfloat16)
+    xn = blk.ff_norm(og)
+    g = torch.nn.functional.silu(xn.float() @ blk.ff_proj.weight.float().t()).to(torch.bfloat16)
+    u = (xn.float() @ blk.up_proj.weight.float().t()).to(torch.bfloat16)
+    hidden = (g.float() * u.float()).to(torch.bfloat16)
+    ref = og.float() + hidden.float() @ blk.ff_out.weight.float().t()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(split.squeeze(0).float(), single.squeeze(0).float(), atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(split.squeeze(0).float(), ref, atol=5e-2, rtol=2e-2)
