@@ -235,7 +235,8 @@ class AttnPlan:
 def make_plan(seqs: list[SeqRows], page_table: np.ndarray, page_log2: int = DEFAULT_PAGE_LOG2,
               device=None, max_rows: int = MAX_TILE_ROWS) -> AttnPlan:
     work, row_idx, n_long, n_mid = build_work(seqs, max_rows)
-    plan = AttnPlan(work=work, row_idx=row_idx, page_table=np.ascontiguousarray(page_table, dtype=np.int32),
+    # the plan owns a copy: a caller may edit its table (a paged pool's refill) afterwards
+    plan = AttnPlan(work=work, row_idx=row_idx, page_table=np.array(page_table, dtype=np.int32),
                     page_log2=page_log2, n_long=n_long, n_mid=n_mid)
     if device is not None:
         plan.to(device)
