@@ -83,6 +83,15 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_softmax_confidence", None, 4, 12, None, None, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_softmax_confidence", None, 4, 16, None, None, None, None)
     lib.call("fdl_softmax_confidence", None, 0, 16, None, None, None, None)  # zero rows: no-op
+    # every other entry point: an empty call returns before any pointer is read
+    lib.call("fdl_importance_rank", None, 10, None, 10, None, 0, 16, None, 0, None)
+    lib.call("fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 5, None, None, 10,
+             None, 10, None, 0, 16, None, 0, None)
+    lib.call("fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 0, 1.0, None, None)
+    lib.call("fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32, 128, None, 0,
+             None, 0, None, 64, 0.1, None, None)
+    lib.call("fdl_rms_norm", None, None, None, 0, 4096, 1e-5, None, None, None)
+    lib.call("fdl_silu_mul", None, None, 0, None, None)
 
 
 def test_gate_up_weights_share_one_buffer():
