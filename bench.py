@@ -184,6 +184,65 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     return dict(Q=Q, total_ms=total_ms, per_kernel_us=per)
 
 
+def run_torch_layer(reps: int = 20, seed: int = 2) -> dict:
+    """The same single-layer chain with unfused PyTorch ops on the same GPU (the
+    conventional path the reference's fused kernels are compared with), batched over the
+    sequences (all 8 have 64 query rows and 768 keys): F.linear Q/K/V, rotate-half RoPE on
+    gathered sin/cos rows, index_copy_ into the caches, K/V head slices gathered from the
+    caches, one batched QK^T and one PV product (bf16, contiguous operands; float32
+    softmax), softmax column sums of the masked rows into the scores, then a sort of each
+    sequence's decoded slots and its top-32."""
+    import torch
+    import torch.nn.functional as F
+    from fdl.torch_path import _rotate
+
+    dev = torch.device("cuda:0")
+    host, d = build_workload(seed, dev)
+    bf = torch.bfloat16
+    slots = d["slot"]
+    kc = torch.zeros((B * L, D), dtype=bf, device=dev)
+    vc = torch.zeros_like(kc)
+    pre = torch.from_numpy(np.concatenate([b * L + np.arange(K_END) for b in range(B)])).to(dev)
+    sp, cp = d["sin"][pre], d["cos"][pre]
+    kc.index_copy_(0, pre, _rotate(F.linear(d["x_prefill"], d["wk"]), sp, cp, H).to(bf))
+    vc.index_copy_(0, pre, F.linear(d["x_prefill"], d["wv"]))
+    sin_r, cos_r = d["sin"][slots], d["cos"][slots]
+    scale = 1.0 / np.sqrt(HD)
+    mb, tb = host["mb"], host["tb"]
+    rows = torch.from_numpy(np.stack([np.concatenate([np.arange(mb[b][2], mb[b][3]),
+                                                      np.arange(tb[b][2], tb[b][3])])
+                                      for b in range(B)])).to(dev)          # [B, 64]
+    nr = rows.shape[1]
+    decoded = [torch.arange(b * L, b * L + int(f), device=dev) for b, f in enumerate(host["frontier"])]
+
+    def step():
+        x = d["x"]
+        q = _rotate(F.linear(x, d["wq"]), sin_r, cos_r, H).to(bf)
+        k = _rotate(F.linear(x, d["wk"]), sin_r, cos_r, H).to(bf)
+        v = F.linear(x, d["wv"])
+        kc.index_copy_(0, slots, k)
+        vc.index_copy_(0, slots, v)
+        kt = kc.view(B, L, H, HD)[:, :K_END].permute(0, 2, 3, 1).contiguous()  # [B, H, hd, K]
+        vh = vc.view(B, L, H, HD)[:, :K_END].permute(0, 2, 1, 3).contiguous()  # [B, H, K, hd]
+        qh = q[rows].view(B, nr, H, HD).permute(0, 2, 1, 3).contiguous()       # [B, H, 64, hd]
+        p = torch.softmax(torch.matmul(qh, kt).float() * scale, dim=-1)
+        o = torch.matmul(p.to(bf), vh)
+        att = torch.empty_like(q)
+        att[rows.reshape(-1)] = o.permute(0, 2, 1, 3).reshape(B * nr, D)
+        colsum = p[:, :, :BM].sum(dim=(1, 2))                                  # [B, K]
+        scores = torch.zeros(B, L, dtype=torch.float32, device=dev)
+        scores[:, :K_END] += colsum
+        scores = scores.view(-1)
+        for b in range(B):
+            order = torch.sort(scores[decoded[b]]).indices
+            decoded[b][order[-TOPK:]]
+        return att
+
+    us = _time_op(step, reps)
+    return {"us": round(us, 2), "what": "the same layer chain with unfused PyTorch ops batched "
+            "over the sequences (conventional path), same GPU, events over " + str(reps) + " steps"}
+
+
 def _time_op(fn, reps: int, warm: int = 3) -> float:
     """Mean microseconds per call of fn() on the current stream (events around the loop)."""
     import torch
@@ -448,6 +507,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-e2e", action="store_true", help="skip the LLaDA-8B decode leg")
+    ap.add_argument("--no-torch", action="store_true",
+                    help="skip the unfused PyTorch timing of the same layer")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the block-table stress and Flash-Verify measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -515,6 +576,10 @@ def main() -> int:
                      "traffic_source": TRAFFIC_FILE.name},
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
+    if not args.no_torch:
+        tl = run_torch_layer()
+        tl["speedup_of_this_build"] = round(tl["us"] / us_layer, 2)
+        out["torch_gpu_layer"] = tl
     if not args.no_configs:
         out["configs"] = run_configs()
     if not args.no_e2e:
