@@ -175,6 +175,34 @@ __device__ __forceinline__ float sum_q_rows(const AttnArgs& a, int roff, int n, 
   return acc;
 }
 
+// Raw importance is linear in Q: the column sums over the importance rows of Q K^T are
+// (sum of those rows' Q) K^T. The fp32 sum x is split into three bf16 parts, hi = bf16(x),
+// mid = bf16(x - hi), lo = bf16(x - hi - mid) (x - hi - mid - lo is below 2^-24 |x|), put in
+// rows 0-2 of one 16-row MFMA A operand; the other rows are zero. Fragment sd covers head
+// columns 32 sd .. 32 sd + 31: lane (l16, g) holds columns 32 sd + 8 g .. + 7 of row l16.
+__device__ __forceinline__ u32x4 qsum_fragment(const float* qsum, int sd, int l16, int g) {
+  u32x4 w = {0, 0, 0, 0};
+  if (l16 < 3) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float x = qsum[32 * sd + 8 * g + 2 * j + e];
+        const float hi = bf2f(f2bf(x));
+        const float mid = bf2f(f2bf(x - hi));
+        v[e] = l16 == 0 ? hi : l16 == 1 ? mid : x - hi - mid;
+      }
+      w[j] = pack_bf16x2(v[0], v[1]);
+    }
+  }
+  return w;
+}
+
+// The dot product of the summed Q with a key from the MFMA result of qsum_fragment rows:
+// lanes g == 0 hold rows 0-3 in acc[0..3]; the parts are added smallest first.
+__device__ __forceinline__ float qsum_dot(const f32x4& acc) { return acc[0] + (acc[1] + acc[2]); }
+
 // Running maxima are raised lazily: a row keeps its reference maximum until a block's
 // logits exceed it by more than kLazyMax (log2 domain, a factor of 256), so the rescale of
 // O and l is skipped for most blocks. Probabilities then stay below 256 (fp32 and bf16
@@ -534,30 +562,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     }
   };
 
-  // Raw importance is linear in Q: the column sums over the importance rows of Q K^T are
-  // (sum of those rows' Q) K^T. The fp32 sum is split into bf16 hi + lo parts, rows 0 and 1
-  // of one 16-row MFMA operand, so one wavefront per block computes all 64 sums.
+  // Raw importance from the summed Q (qsum_fragment): one wavefront per block computes all
+  // 64 column sums.
   if (imp_raw && tid < kHeadDim) qsum_buf[tid] = sum_q_rows(a, roff, n_imp, D, col0 + tid);
   barrier_lds_drained();  // #0
-  // A-operand fragment sd of the summed Q: row 0 (lane l16 == 0) the bf16 part, row 1 the
-  // remainder, other rows zero; built once by wave sd.
-  if (imp_raw && wr < 4) {
-    u32x4 w = {0, 0, 0, 0};
-    if (l16 < 2) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float x = qsum_buf[32 * wr + 8 * g + 2 * j + e];
-          const float hi = bf2f(f2bf(x));
-          v[e] = l16 == 0 ? hi : x - hi;
-        }
-        w[j] = pack_bf16x2(v[0], v[1]);
-      }
-    }
-    qsum_frag_buf[wr][lane] = w;
-  }
+  // A-operand fragment sd of the summed Q (rows 0-2 its three bf16 parts), built by wave sd
+  if (imp_raw && wr < 4) qsum_frag_buf[wr][lane] = qsum_fragment(qsum_buf, wr, l16, g);
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
   for (int s = 0; s < n_steps; ++s) {
@@ -614,7 +624,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
           acc = mfma16(as_bf16x8(qsum_frag_buf[sd][lane]), k_frag(kt, wr, sd, l16, g), acc);
         const int n = n0 + 16 * wr + l16;
         if (g == 0 && n < k_end) {
-          const float v = acc[0] + acc[1];  // rows hi + lo
+          const float v = qsum_dot(acc);
           if constexpr (!kStore && !kVerify) {
             if (slots_staged) raw_buf[n - k_begin] = v;
             else imp_out[slot_of(n)] = v;
@@ -955,24 +965,8 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
   }
   if (imp_raw && tid < kHeadDim) qsum_buf[tid] = sum_q_rows(a, roff, n_imp, D, col0 + tid);
   __syncthreads();
-  // raw importance: summed Q as bf16 hi + lo rows of one MFMA operand (see attn_kernel)
-  if (imp_raw && wave < 4) {
-    u32x4 w = {0, 0, 0, 0};
-    if (l16 < 2) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float x = qsum_buf[32 * wave + 8 * g + 2 * j + e];
-          const float hi = bf2f(f2bf(x));
-          v[e] = l16 == 0 ? hi : x - hi;
-        }
-        w[j] = pack_bf16x2(v[0], v[1]);
-      }
-    }
-    qsum_frag_buf[wave][lane] = w;
-  }
+  // raw importance: summed Q as three bf16 rows of one MFMA operand (see attn_kernel)
+  if (imp_raw && wave < 4) qsum_frag_buf[wave][lane] = qsum_fragment(qsum_buf, wave, l16, g);
   // The Q loads are waited for here, before the first block load is issued: a later wait
   // the compiler places for them would also wait for every block load issued since.
 #pragma unroll
@@ -1066,7 +1060,7 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
             for (int sd = 0; sd < 4; ++sd)
               acc = mfma16(qs[sd], k_frag(kt, wave, sd, l16, g), acc);
             const int n = k_begin + kTileN * p + 16 * wave + l16;
-            if (g == 0 && n < k_end) imp_out[slot_of(n)] = acc[0] + acc[1];
+            if (g == 0 && n < k_end) imp_out[slot_of(n)] = qsum_dot(acc);
           }
         };
         long_qk(sc, qf, kt_of(0), l16, g);
@@ -1257,8 +1251,7 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   // kernel on each half of an item (the importance rows lie in the first half)
   hipError_t e;
   if (tile_rows == 64) {
-    e = imp_mode == FDL_IMP_SOFTMAX_COLSUM ? launch_attn<1, 4, false, true>(args, n_work, n_heads, s)
-                                           : launch_attn<1, 4, false>(args, n_work, n_heads, s);
+    e = launch_attn<1, 4, false>(args, n_work, n_heads, s);
   } else if (tile_rows == 128) {
     e = launch_attn<1, 8, false>(args, n_work, n_heads, s);
   } else if (imp_mode == FDL_IMP_SOFTMAX_COLSUM) {

@@ -53,12 +53,20 @@ from .schedule import (DEFAULT_PAGE_LOG2, PagePool, SeqRows, contiguous_page_tab
 
 
 def get_rotary_embedding(seq_len: int, dim: int, rope_theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """sin, cos float32 [seq_len, dim] (llada/generate.py:44-50)."""
-    inv_freq = 1.0 / (rope_theta ** (torch.arange(0, dim, 2, device=device, dtype=torch.float32) / dim))
-    seq = torch.arange(seq_len, device=device, dtype=torch.float32)
-    freqs = torch.outer(seq, inv_freq)
-    positions = torch.cat((freqs, freqs), dim=-1)
-    return positions.sin(), positions.cos()
+    """sin, cos float32 [seq_len, dim] (llada/generate.py:44-50).
+
+    The reference's float32 steps (inv_freq = 1 / theta^(arange(0, dim, 2) / dim), freqs =
+    p * inv_freq, cat(freqs, freqs) -> sin, cos), each correctly rounded: every step is
+    evaluated in float64 and rounded to float32 once, so the table does not depend on the
+    device's float32 pow and sin (which may be an ulp or two off; an ulp of inv_freq moves
+    the angle at position 900 by ~5e-5)."""
+    f64 = torch.float64
+    e = torch.arange(0, dim, 2, device=device, dtype=torch.float32) / dim
+    inv_freq = (1.0 / (rope_theta ** e.to(f64)).float().to(f64)).float()
+    seq = torch.arange(seq_len, device=device, dtype=f64)
+    freqs = torch.outer(seq, inv_freq.to(f64)).float()
+    positions = torch.cat((freqs, freqs), dim=-1).to(f64)
+    return positions.sin().float(), positions.cos().float()
 
 
 def make_blocks(j: int, seqlen_k, start_m: int, end_m: int, block_m: int) -> np.ndarray:

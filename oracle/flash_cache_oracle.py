@@ -24,6 +24,8 @@ How each function is pinned (tests/test_oracle_*.py):
   importance_raw_S     (sum_r q_r) . k_n closed form per head                (pinned)
   importance_accumulate  S.mean((0, 1)) of that closed form, same test       (pinned)
   importance_softmax   explicit softmax-matrix column sums                   (pinned)
+  importance_f64       raw: exact rational sum (math.fsum of every product);
+                       softmax: torch float64 softmax column sums            (pinned)
   verify_attention     torch SDPA with a boolean mask over gathered keys     (pinned)
   verify_mask          hand-worked matrices for (T, S) = (2, 3), (0, 2)      (pinned)
   rank_ascending/topk  brute force with Python sorted() on (score, slot)     (pinned)
@@ -48,13 +50,18 @@ F32 = np.float32
 def rope_tables(seq_len: int, head_dim: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
     """sin, cos float32 [seq_len, head_dim] (llada/generate.py:44-50).
 
-    inv_freq = 1 / theta^(arange(0, hd, 2)/hd); freqs = p (x) inv_freq;
-    table = cat(freqs, freqs) -> sin, cos. Computed in float32 like the reference.
+    The reference's float32 steps, each correctly rounded (what an exact float32 libm
+    gives; the reference's own values depend on its device's pow/sin):
+      e = fl(arange(0, hd, 2) / hd); inv_freq = fl(1 / fl(theta ** e));
+      freqs = fl(p * inv_freq); table = cat(freqs, freqs) -> fl(sin), fl(cos).
+    Every step is evaluated in float64 and rounded to float32 once.
     """
-    inv_freq = (F32(1.0) / (F32(theta) ** (np.arange(0, head_dim, 2, dtype=F32) / F32(head_dim)))).astype(F32)
-    seq = np.arange(seq_len, dtype=F32)
-    freqs = np.outer(seq, inv_freq).astype(F32)
-    pos = np.concatenate([freqs, freqs], axis=-1)
+    e = np.arange(0, head_dim, 2, dtype=F32) / F32(head_dim)
+    pw = (np.float64(theta) ** e.astype(np.float64)).astype(F32)
+    inv_freq = (1.0 / pw.astype(np.float64)).astype(F32)
+    seq = np.arange(seq_len, dtype=np.float64)
+    freqs = (seq[:, None] * inv_freq.astype(np.float64)[None, :]).astype(F32)
+    pos = np.concatenate([freqs, freqs], axis=-1).astype(np.float64)
     return np.sin(pos).astype(F32), np.cos(pos).astype(F32)
 
 
@@ -203,6 +210,40 @@ def importance_softmax_colsum(q: np.ndarray, k_cache: np.ndarray, masked_blocks:
             s = (q[q0:q1, cols].astype(F32) @ k_cache[slots][:, cols].astype(F32).T) * F32(scale)
             scores[b * max_length: b * max_length + k_end] += _softmax_rows(s).sum(axis=0)
     return scores.astype(F32)
+
+
+def importance_f64(q: np.ndarray, k_cache: np.ndarray, masked_blocks: np.ndarray,
+                   n_batch: int, max_length: int, n_heads: int, mode: str, scale: float,
+                   block_m: int, page_table: np.ndarray | None = None,
+                   page_size: int = 32) -> np.ndarray:
+    """One layer's importance scores in float64, the exact values that the float32 kernels
+    approximate: float64 [n_batch * max_length], zero outside the masked blocks' keys.
+
+    mode "raw":     mean over (block_m rows, heads) of S[r, h, b, n] = q_r^h . k_n^h
+                    (flash_cache_triton.py:155-158 written, :614-615 reduced; rows past q1
+                    of a ragged block are zero in S and still count in the mean).
+    mode "softmax": sum over heads and rows r of softmax_n(scale q_r^h . k_n^h), the
+                    column-sum definition of the importance.
+    """
+    d_model = q.shape[1]
+    hd = d_model // n_heads
+    scores = np.zeros(n_batch * max_length, dtype=np.float64)
+    for b, k_end, q0, q1 in np.asarray(masked_blocks, dtype=np.int64):
+        slots = key_slots(int(b), int(k_end), max_length, page_table, page_size)
+        acc = np.zeros(int(k_end), dtype=np.float64)
+        for h in range(n_heads):
+            cols = slice(h * hd, (h + 1) * hd)
+            s = q[q0:q1, cols].astype(np.float64) @ k_cache[slots][:, cols].astype(np.float64).T
+            if mode == "raw":
+                acc += s.sum(axis=0)
+            else:
+                s = s * scale
+                e = np.exp(s - s.max(axis=1, keepdims=True))
+                acc += (e / e.sum(axis=1, keepdims=True)).sum(axis=0)
+        if mode == "raw":
+            acc /= block_m * n_heads
+        scores[slots] += acc
+    return scores
 
 
 # --------------------------------------------------------------------------------------

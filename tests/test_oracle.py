@@ -188,6 +188,44 @@ def test_importance_softmax_colsum_vs_torch_softmax():
     assert abs(got.sum() - 4 * n_heads) < 1e-4  # each row's probabilities sum to one
 
 
+def test_importance_f64_raw_exact_sum():
+    """float64 raw importance = the exact mean of every product q_r^h[d] k_n^h[d] (math.fsum
+    is exactly rounded), ragged blocks counting block_m rows, keys past k_end untouched."""
+    import math
+    gen = torch.Generator().manual_seed(16)
+    n_heads, hd, B, L, bm = 3, 128, 2, 64, 4
+    D = n_heads * hd
+    kc = _bf16_np((B * L, D), gen)
+    q = _bf16_np((7, D), gen)
+    masked = np.array([[0, 40, 0, 4], [1, 64, 4, 7]])  # the second block has 3 of 4 rows
+    got = orc.importance_f64(q, kc, masked, B, L, n_heads, "raw", 0.0, bm)
+    for b, k_end, q0, q1 in masked:
+        for n in (0, 5, k_end - 1):
+            terms = [float(q[r, d]) * float(kc[b * L + n, d]) for r in range(q0, q1) for d in range(D)]
+            assert abs(got[b * L + n] - math.fsum(terms) / (bm * n_heads)) <= 1e-12 * (1 + abs(got[b * L + n]))
+    assert np.all(got[40:L] == 0)
+
+
+def test_importance_f64_softmax_vs_torch_float64():
+    gen = torch.Generator().manual_seed(17)
+    n_heads, hd, B, L = 2, 128, 2, 64
+    D = n_heads * hd
+    kc = _bf16_np((B * L, D), gen)
+    q = _bf16_np((6, D), gen)
+    scale = orc.softmax_scale(hd)
+    masked = np.array([[0, 50, 0, 3], [1, 64, 3, 6]])
+    got = orc.importance_f64(q, kc, masked, B, L, n_heads, "softmax", scale, 32)
+    exp = np.zeros(B * L)
+    for b, k_end, q0, q1 in masked:
+        for h in range(n_heads):
+            cols = slice(h * hd, (h + 1) * hd)
+            s = torch.from_numpy(q[q0:q1, cols]).double() @ torch.from_numpy(kc[b * L:b * L + k_end, cols]).double().T
+            exp[b * L:b * L + k_end] += torch.softmax(s * scale, dim=1).sum(0).numpy()
+    np.testing.assert_allclose(got, exp, rtol=1e-13, atol=1e-15)
+    # each row's probabilities sum to one, for every head
+    assert abs(got.sum() - 6 * n_heads) < 1e-12
+
+
 # --------------------------------------------------------------------------- verify
 
 def test_verify_mask_kat_T2_S3():
