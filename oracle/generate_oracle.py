@@ -10,7 +10,20 @@ reference leaves open are the two sort tie rules:
     highest-ranked tail prefers lower slots).
 It calls `model(x_query, use_cache=True, lengths=..., positions=...)` exactly like the
 reference and reads all logits rows. The tokenizer-dependent text handling (:385-402) is
-replaced by storing the generated token ids.
+replaced by storing the generated token ids. The RoPE tables are the correctly rounded
+float32 tables of flash_cache_oracle.rope_tables (:44-50).
+
+How it is pinned (tests/test_generate_kat.py): a scripted model sets every logit row's
+float64 softmax maximum and every importance score, and the decisions are checked against
+values worked out by hand from the reference's rules:
+  pass-1 acceptance   max(#conf >= threshold, 1), the EOS length mask zeroing confidences
+                      at or past the predicted length (a 0.95 there must lose)     (pinned)
+  refresh order       ascending scores, ties to the higher slot                    (pinned)
+  tracked set         track_num 1, 2, -1 and a mask_num 2 look-ahead window        (pinned)
+  verify lists, mask  fill/draft/mask rows, key list and m11..m22 for (T, S) = (4, 2),
+                      the candidate-free (8, 0) case                                (pinned)
+  verify acceptance   cumprod prefix >= gamma (0.95, 0.92 -> 1 accepted, not 2)    (pinned)
+  refill              the next prompt loaded into the finished row                  (pinned)
 """
 from __future__ import annotations
 
@@ -30,12 +43,10 @@ def _make_blocks(j, seqlen_k, start_m, end_m, block_m, device):
 
 
 def _rope(seq_len, dim, theta, device):
-    """llada/generate.py:44-50."""
-    inv_freq = 1.0 / (theta ** (torch.arange(0, dim, 2, device=device, dtype=torch.float32) / dim))
-    seq = torch.arange(seq_len, device=device, dtype=torch.float32)
-    freqs = torch.outer(seq, inv_freq)
-    positions = torch.cat((freqs, freqs), dim=-1)
-    return positions.sin(), positions.cos()
+    """llada/generate.py:44-50, correctly rounded (flash_cache_oracle.rope_tables)."""
+    from .flash_cache_oracle import rope_tables
+    sin, cos = rope_tables(seq_len, dim, theta)
+    return torch.from_numpy(sin).to(device), torch.from_numpy(cos).to(device)
 
 
 def _stable_desc(v: torch.Tensor) -> torch.Tensor:
