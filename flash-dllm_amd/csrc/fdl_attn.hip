@@ -32,6 +32,7 @@
 #include "fdl_device.h"
 #include "fdl_host.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace fdl {
@@ -1196,36 +1197,35 @@ hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, h
 }  // namespace
 }  // namespace fdl
 
-extern "C" int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
-                                   int64_t n_q_rows, int64_t n_slots, int64_t d_model,
-                                   int64_t n_heads, int64_t head_dim,
-                                   const int32_t* page_table, int64_t n_seq, int64_t max_pages,
-                                   int32_t page_log2, const int32_t* work, int64_t n_work,
-                                   const int32_t* row_idx, int64_t n_row_idx, int32_t tile_rows,
-                                   float softmax_scale, void* out, int32_t imp_mode,
-                                   float* imp_part, void* stream) {
-  using namespace fdl;
-  FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
-              "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
-  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, FDL_ERR_UNSUPPORTED,
-              "fdl_block_attention: tile_rows = %d (64, 128 or 256)", tile_rows);
-  if (n_work == 0) return ok();
-  int rc = check_common("fdl_block_attention", q, k_cache, v_cache, out, d_model, n_heads,
-                        head_dim);
+namespace fdl {
+namespace {
+
+#define FDL_REQUIRE_ARG(p) FDL_REQUIRE((p) != nullptr, FDL_ERR_NULL, "%s: %s is NULL", fn, #p)
+
+// Checks the arguments of a block-attention call and enqueues its kernels (the shared body
+// of fdl_block_attention and fdl_block_attention_scores_noalloc).
+int block_attention_launch(const char* fn, const void* q, const void* k_cache, const void* v_cache,
+                           int64_t n_q_rows, int64_t n_slots, int64_t d_model, int64_t n_heads,
+                           int64_t head_dim, const int32_t* page_table, int64_t n_seq,
+                           int64_t max_pages, int32_t page_log2, const int32_t* work,
+                           int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
+                           int32_t tile_rows, float softmax_scale, void* out, int32_t imp_mode,
+                           float* imp_part, hipStream_t s) {
+  int rc = check_common(fn, q, k_cache, v_cache, out, d_model, n_heads, head_dim);
   if (rc != FDL_OK) return rc;
-  FDL_REQUIRE_PTR(page_table);
-  FDL_REQUIRE_PTR(work);
-  FDL_REQUIRE_PTR(row_idx);
+  FDL_REQUIRE_ARG(page_table);
+  FDL_REQUIRE_ARG(work);
+  FDL_REQUIRE_ARG(row_idx);
   FDL_REQUIRE(n_seq >= 1 && max_pages >= 1 && n_slots >= 1 && n_q_rows >= 1 && n_row_idx >= 1,
-              FDL_ERR_SHAPE, "fdl_block_attention: empty table or cache");
+              FDL_ERR_SHAPE, "%s: empty table or cache", fn);
   FDL_REQUIRE(page_log2 >= 4 && page_log2 <= 12, FDL_ERR_SHAPE,
-              "fdl_block_attention: page_log2 = %d outside [4, 12]", page_log2);
+              "%s: page_log2 = %d outside [4, 12]", fn, page_log2);
   FDL_REQUIRE(max_pages << page_log2 < (int64_t(1) << 31) && n_seq < (int64_t(1) << 31),
-              FDL_ERR_SHAPE, "fdl_block_attention: max_pages or n_seq too large");
+              FDL_ERR_SHAPE, "%s: max_pages or n_seq too large", fn);
   FDL_REQUIRE(imp_mode >= FDL_IMP_NONE && imp_mode <= FDL_IMP_SOFTMAX_COLSUM, FDL_ERR_SHAPE,
-              "fdl_block_attention: imp_mode = %d unknown", imp_mode);
+              "%s: imp_mode = %d unknown", fn, imp_mode);
   FDL_REQUIRE(imp_mode == FDL_IMP_NONE || imp_part != nullptr, FDL_ERR_NULL,
-              "fdl_block_attention: imp_part is NULL with imp_mode = %d", imp_mode);
+              "%s: imp_part is NULL with imp_mode = %d", fn, imp_mode);
   AttnArgs args = {};
   args.q = static_cast<const uint16_t*>(q);
   args.k = static_cast<const uint16_t*>(k_cache);
@@ -1245,7 +1245,6 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   args.tile_rows = tile_rows;
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   // 64-row tiles: four consumers of 16 rows; 128-row tiles: eight consumers (two per SIMD);
   // 256-row tiles: the two-group kernel, or with softmax-colsum importance the 128-row
   // kernel on each half of an item (the importance rows lie in the first half)
@@ -1256,12 +1255,12 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
     e = launch_attn<1, 8, false>(args, n_work, n_heads, s);
   } else if (imp_mode == FDL_IMP_SOFTMAX_COLSUM) {
     FDL_REQUIRE(n_work < (int64_t(1) << 30), FDL_ERR_SHAPE,
-                "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
+                "%s: n_work = %lld out of range", fn, (long long)n_work);
     args.split = 1;
     e = launch_attn<1, 8, false>(args, 2 * n_work, n_heads, s);
   } else {
     FDL_REQUIRE(n_work * n_heads < (int64_t(1) << 31), FDL_ERR_SHAPE,
-                "fdl_block_attention: %lld items x %lld heads out of range", (long long)n_work,
+                "%s: %lld items x %lld heads out of range", fn, (long long)n_work,
                 (long long)n_heads);
     args.n_items = static_cast<int>(n_work);
     hipLaunchKernelGGL(attn_long_kernel, dim3(static_cast<unsigned>(n_work * n_heads)),
@@ -1269,7 +1268,127 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
     e = hipGetLastError();
   }
   FDL_HIP_CHECK(e);
-  return ok();
+  return FDL_OK;
+}
+
+int importance_accumulate_launch(const char* fn, const float* imp_part, int64_t n_heads,
+                                 int64_t n_slots, const int32_t* page_table, int64_t n_seq,
+                                 int64_t max_pages, int32_t page_log2, const int32_t* work,
+                                 int64_t n_work, float scale, float* scores, hipStream_t s) {
+  FDL_REQUIRE(n_work >= 0 && n_work < 65536, FDL_ERR_SHAPE, "%s: n_work = %lld out of range", fn,
+              (long long)n_work);
+  if (n_work == 0) return FDL_OK;
+  FDL_REQUIRE_ARG(imp_part);
+  FDL_REQUIRE_ARG(page_table);
+  FDL_REQUIRE_ARG(work);
+  FDL_REQUIRE_ARG(scores);
+  FDL_REQUIRE(n_heads >= 1 && n_slots >= 1 && n_seq >= 1 && max_pages >= 1, FDL_ERR_SHAPE,
+              "%s: empty dimension", fn);
+  FDL_REQUIRE(page_log2 >= 4 && page_log2 <= 12, FDL_ERR_SHAPE,
+              "%s: page_log2 = %d outside [4, 12]", fn, page_log2);
+  hipLaunchKernelGGL(imp_accumulate_kernel, dim3(4, static_cast<unsigned>(n_work)), dim3(256), 0,
+                     s, imp_part, static_cast<int>(n_heads), n_slots, page_table,
+                     static_cast<int>(n_seq), static_cast<int>(max_pages), page_log2, work, scale,
+                     scores);
+  FDL_HIP_CHECK(hipGetLastError());
+  return FDL_OK;
+}
+
+// Library-owned device memory of fdl_block_attention_scores_noalloc: the per-head importance
+// partials [n_heads][n_slots] (fp32). Every GPU the library runs on holds its own copy from
+// module load until the process ends. In host code `scratch` names a host-side stand-in, not
+// a device address: kernels get the address that hipGetSymbolAddress returns for the current
+// device (scratch_on_current_device).
+constexpr int64_t kScratchFloats = FDL_NOALLOC_SCRATCH_BYTES / 4;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device.
+int scratch_on_current_device(float** ptr) {
+  int dev = -1;
+  FDL_HIP_CHECK(hipGetDevice(&dev));
+  FDL_REQUIRE(dev >= 0 && dev < kMaxDevices, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention_scores_noalloc: device %d beyond the %d supported", dev,
+              kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    FDL_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    FDL_REQUIRE(p != nullptr, FDL_ERR_HIP,
+                "fdl_block_attention_scores_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return FDL_OK;
+}
+
+}  // namespace
+}  // namespace fdl
+
+extern "C" int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
+                                   int64_t n_q_rows, int64_t n_slots, int64_t d_model,
+                                   int64_t n_heads, int64_t head_dim,
+                                   const int32_t* page_table, int64_t n_seq, int64_t max_pages,
+                                   int32_t page_log2, const int32_t* work, int64_t n_work,
+                                   const int32_t* row_idx, int64_t n_row_idx, int32_t tile_rows,
+                                   float softmax_scale, void* out, int32_t imp_mode,
+                                   float* imp_part, void* stream) {
+  using namespace fdl;
+  FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
+              "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
+  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention: tile_rows = %d (64, 128 or 256)", tile_rows);
+  if (n_work == 0) return ok();
+  const int rc = block_attention_launch("fdl_block_attention", q, k_cache, v_cache, n_q_rows, n_slots, d_model, n_heads,
+                                        head_dim, page_table, n_seq, max_pages, page_log2, work,
+                                        n_work, row_idx, n_row_idx, tile_rows, softmax_scale, out,
+                                        imp_mode, imp_part, static_cast<hipStream_t>(stream));
+  return rc == FDL_OK ? ok() : rc;
+}
+
+extern "C" int fdl_block_attention_scores_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, int64_t n_q_rows, int64_t n_slots,
+    int64_t d_model, int64_t n_heads, int64_t head_dim, const int32_t* page_table, int64_t n_seq,
+    int64_t max_pages, int32_t page_log2, const int32_t* work, int64_t n_work,
+    const int32_t* row_idx, int64_t n_row_idx, int32_t tile_rows, float softmax_scale, void* out,
+    int32_t imp_mode, float imp_scale, float* scores, void* stream) {
+  using namespace fdl;
+  FDL_REQUIRE(n_work >= 0 && n_work < 65536, FDL_ERR_SHAPE,
+              "fdl_block_attention_scores_noalloc: n_work = %lld out of range",
+              (long long)n_work);
+  FDL_REQUIRE(tile_rows == 64 || tile_rows == 128 || tile_rows == 256, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention_scores_noalloc: tile_rows = %d (64, 128 or 256)", tile_rows);
+  FDL_REQUIRE(imp_mode >= FDL_IMP_NONE && imp_mode <= FDL_IMP_SOFTMAX_COLSUM, FDL_ERR_SHAPE,
+              "fdl_block_attention_scores_noalloc: imp_mode = %d unknown", imp_mode);
+  FDL_REQUIRE(n_heads >= 1 && n_slots >= 1, FDL_ERR_SHAPE,
+              "fdl_block_attention_scores_noalloc: empty dimension");
+  FDL_REQUIRE(imp_mode == FDL_IMP_NONE || n_heads <= kScratchFloats / n_slots, FDL_ERR_UNSUPPORTED,
+              "fdl_block_attention_scores_noalloc: %lld heads x %lld slots of importance "
+              "partials exceed the %lld-byte scratch (FDL_NOALLOC_SCRATCH_BYTES)",
+              (long long)n_heads, (long long)n_slots, (long long)FDL_NOALLOC_SCRATCH_BYTES);
+  FDL_REQUIRE(imp_mode == FDL_IMP_NONE || scores != nullptr, FDL_ERR_NULL,
+              "fdl_block_attention_scores_noalloc: scores is NULL with imp_mode = %d", imp_mode);
+  if (n_work == 0) return ok();
+  float* part = nullptr;
+  if (imp_mode != FDL_IMP_NONE) {
+    const int rc = scratch_on_current_device(&part);
+    if (rc != FDL_OK) return rc;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // every partial the reduction reads is written by the attention first (the keys of the
+  // importance tiles), so the scratch needs no clearing between calls
+  int rc = block_attention_launch("fdl_block_attention_scores_noalloc", q, k_cache, v_cache,
+                                  n_q_rows, n_slots, d_model, n_heads,
+                                  head_dim, page_table, n_seq, max_pages, page_log2, work, n_work,
+                                  row_idx, n_row_idx, tile_rows, softmax_scale, out, imp_mode,
+                                  part, s);
+  if (rc == FDL_OK && imp_mode != FDL_IMP_NONE)
+    rc = importance_accumulate_launch("fdl_block_attention_scores_noalloc", part, n_heads, n_slots, page_table, n_seq, max_pages,
+                                      page_log2, work, n_work, imp_scale, scores, s);
+  return rc == FDL_OK ? ok() : rc;
 }
 
 extern "C" int fdl_importance_accumulate(const float* imp_part, int64_t n_heads, int64_t n_slots,
@@ -1278,23 +1397,11 @@ extern "C" int fdl_importance_accumulate(const float* imp_part, int64_t n_heads,
                                          const int32_t* work, int64_t n_work, float scale,
                                          float* scores, void* stream) {
   using namespace fdl;
-  FDL_REQUIRE(n_work >= 0 && n_work < 65536, FDL_ERR_SHAPE,
-              "fdl_importance_accumulate: n_work = %lld out of range", (long long)n_work);
-  if (n_work == 0) return ok();
-  FDL_REQUIRE_PTR(imp_part);
-  FDL_REQUIRE_PTR(page_table);
-  FDL_REQUIRE_PTR(work);
-  FDL_REQUIRE_PTR(scores);
-  FDL_REQUIRE(n_heads >= 1 && n_slots >= 1 && n_seq >= 1 && max_pages >= 1, FDL_ERR_SHAPE,
-              "fdl_importance_accumulate: empty dimension");
-  FDL_REQUIRE(page_log2 >= 4 && page_log2 <= 12, FDL_ERR_SHAPE,
-              "fdl_importance_accumulate: page_log2 = %d outside [4, 12]", page_log2);
-  hipLaunchKernelGGL(imp_accumulate_kernel, dim3(4, static_cast<unsigned>(n_work)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), imp_part, static_cast<int>(n_heads),
-                     n_slots, page_table, static_cast<int>(n_seq), static_cast<int>(max_pages),
-                     page_log2, work, scale, scores);
-  FDL_HIP_CHECK(hipGetLastError());
-  return ok();
+  const int rc = importance_accumulate_launch("fdl_importance_accumulate", imp_part, n_heads,
+                                              n_slots, page_table, n_seq,
+                                              max_pages, page_log2, work, n_work, scale, scores,
+                                              static_cast<hipStream_t>(stream));
+  return rc == FDL_OK ? ok() : rc;
 }
 
 extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void* v_blk,

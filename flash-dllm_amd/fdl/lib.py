@@ -70,6 +70,14 @@ SIGNATURES: dict[str, tuple] = {
         _f32, _p, _i32, _p,           # softmax_scale, out, imp_mode, imp_part
         _p,                           # stream
     ]),
+    "fdl_block_attention_scores_noalloc": (ctypes.c_int, [
+        _p, _p, _p,                   # q, k_cache, v_cache
+        _i64, _i64, _i64, _i64, _i64,  # n_q_rows, n_slots, d_model, n_heads, head_dim
+        _p, _i64, _i64, _i32,         # page_table, n_seq, max_pages, page_log2
+        _p, _i64, _p, _i64, _i32,     # work, n_work, row_idx, n_row_idx, tile_rows
+        _f32, _p, _i32, _f32, _p,     # softmax_scale, out, imp_mode, imp_scale, scores
+        _p,                           # stream
+    ]),
     "fdl_importance_accumulate": (ctypes.c_int, [
         _p, _i64, _i64,               # imp_part, n_heads, n_slots
         _p, _i64, _i64, _i32,         # page_table, n_seq, max_pages, page_log2

@@ -120,6 +120,33 @@ int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
                         float* imp_part, void* stream);
 
 /*
+ * No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops or harnesses that forbid hipMalloc): one call does
+ * fdl_block_attention followed by fdl_importance_accumulate, with the per-head importance
+ * partials in a library-owned static device array of FDL_NOALLOC_SCRATCH_BYTES (32 MiB) on
+ * each GPU, held until the process ends, instead of a caller workspace. The caller still
+ * passes the inputs, `out` and `scores`; nothing is allocated (no hipMalloc/hipFree).
+ *   out     as fdl_block_attention
+ *   scores  fp32 [n_slots], with imp_mode != FDL_IMP_NONE:
+ *           scores[slot(n)] += imp_scale * sum_h (head-h importance of key n), heads summed in
+ *           ascending order: bit for bit what fdl_block_attention + fdl_importance_accumulate
+ *           (scale = imp_scale) leave in scores
+ * Rejects (FDL_ERR_UNSUPPORTED) n_heads * n_slots * 4 bytes beyond FDL_NOALLOC_SCRATCH_BYTES.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (e.g. on two
+ * streams) race on it and must be serialised by the caller.
+ */
+#define FDL_NOALLOC_SCRATCH_BYTES (32LL << 20)
+int fdl_block_attention_scores_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                       int64_t n_q_rows, int64_t n_slots, int64_t d_model,
+                                       int64_t n_heads, int64_t head_dim,
+                                       const int32_t* page_table, int64_t n_seq,
+                                       int64_t max_pages, int32_t page_log2, const int32_t* work,
+                                       int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
+                                       int32_t tile_rows, float softmax_scale, void* out,
+                                       int32_t imp_mode, float imp_scale, float* scores,
+                                       void* stream);
+
+/*
  * scores[slot(n)] += scale * sum_{h = 0..n_heads-1} imp_part[h][slot(n)] for every tile
  * with n_imp > 0 and n in [k_begin, k_end), heads summed in ascending order.
  * Replaces `attn_scores += S.mean((0, 1)).view(-1)` (flash_cache_triton.py:614-615) with
