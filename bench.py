@@ -68,11 +68,9 @@ def build_workload(seed: int, device):
         "wv": (torch.randn((D, D), generator=gen) * 0.02).to(torch.bfloat16),
         "x_prefill": (torch.randn((B * K_END, D), generator=gen)).to(torch.bfloat16),
     }
-    inv = 1.0 / (THETA ** (np.arange(0, HD, 2, dtype=np.float32) / np.float32(HD)))
-    ang = np.outer(np.arange(L, dtype=np.float32), inv.astype(np.float32)).astype(np.float32)
-    ang = np.concatenate([ang, ang], axis=1)
-    sin = np.tile(np.sin(ang).astype(np.float32), (B, 1))
-    cos = np.tile(np.cos(ang).astype(np.float32), (B, 1))
+    sin_l, cos_l = _rope_tables(L)
+    sin = np.tile(sin_l.numpy(), (B, 1))
+    cos = np.tile(cos_l.numpy(), (B, 1))
     host = dict(slots=slots, mb=mb, tb=tb, frontier=frontier, sin=sin, cos=cos, **w)
     dev = None
     if device is not None:
@@ -258,43 +256,55 @@ def _time_op(fn, reps: int, warm: int = 3) -> float:
     return e0.elapsed_time(e1) * 1e3 / reps
 
 
-def run_configs(seed: int = 3, reps: int = 10) -> dict:
-    """Secondary measurements on the other single-layer workloads (bf16, d_model 4096, 32
-    heads): the block-table stress batch (32 sequences, caches of 512-1536 keys in randomly
-    permuted 32-slot pages, a quarter of them full recomputes), its full-recompute tiles on
-    their own, and the Flash-Verify batch (16 sequences, 1024-slot caches, 4-32 candidates
-    each as draft and mask rows). Synthetic N(0,1) activations and N(0,0.02) weights."""
-    import torch
-    from fdl import lib, ops
-    from fdl.generate import verify_mask
-    from fdl.schedule import SeqRows, make_plan
+def _rope_tables(n: int):
+    """sin, cos float32 [n, 128] for positions 0 .. n-1 (the decode loop's tables, on the CPU)."""
+    from fdl.generate import get_rotary_embedding
+    return get_rotary_embedding(n, HD, THETA, "cpu")
 
-    dev = torch.device("cuda:0")
+
+def build_one_sequence(seed: int = 1) -> dict:
+    """One sequence, keys 0..383 (stride 384): the projection of a 32-row masked block at
+    frontier 192 plus 8 tracked slots from [0, 192) (40 rows), then attention of the 40 rows
+    over the 384 keys. Hidden N(0,1), weights N(0,0.02); the cache holds the projected K/V
+    of N(0,1) hidden states at every slot."""
+    import torch
     rng = np.random.default_rng(seed)
     gen = torch.Generator().manual_seed(seed)
-    bf = lambda *shape, std=1.0: (torch.randn(shape, generator=gen) * std).to(torch.bfloat16).to(dev)  # noqa: E731
-    scale = 1.0 / np.sqrt(HD)
-    out = {}
+    Lc = 384
+    slots = np.concatenate([np.arange(192, 224), np.sort(rng.choice(192, 8, replace=False))])
+    w = [(torch.randn((D, D), generator=gen) * 0.02).to(torch.bfloat16) for _ in range(3)]
+    x_pre = torch.randn((Lc, D), generator=gen).to(torch.bfloat16)
+    x = torch.randn((len(slots), D), generator=gen).to(torch.bfloat16)
+    sin, cos = _rope_tables(Lc)
+    return dict(L=Lc, slots=slots.astype(np.int64), w=w, x_pre=x_pre, x=x, sin=sin, cos=cos)
 
-    # --- block-table stress
+
+def build_stress(seed: int = 3) -> dict:
+    """Block-table stress batch: 32 sequences, caches of 512-1536 keys in randomly permuted
+    32-slot pages, a quarter of them full recomputes (query = every key), the others 1-96
+    rows (a masked block of up to 32 at a random frontier, the rest unique decoded slots);
+    RoPE at each row's logical position."""
+    import torch
+    from fdl.schedule import SeqRows
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed)
     NB, P = 32, 32
     k_ends = rng.integers(512, 1537, NB)
     full = rng.random(NB) < 0.25
     pages = [(int(k) + P - 1) // P for k in k_ends]
     n_pages = int(sum(pages))
     perm = rng.permutation(n_pages)
-    max_pages = max(pages)
-    table = np.zeros((NB, max_pages), np.int32)
+    table = np.zeros((NB, max(pages)), np.int32)
     nxt = 0
     for b in range(NB):
         table[b, :pages[b]] = perm[nxt:nxt + pages[b]]
         nxt += pages[b]
-    n_slots = n_pages * P
     seqs, row, slot_list, logical_list = [], 0, [], []
     for b in range(NB):
         k = int(k_ends[b])
-        logical = np.arange(k) if full[b] else None
-        if logical is None:
+        if full[b]:
+            logical = np.arange(k)
+        else:
             qn = int(rng.integers(1, 97))
             m = min(qn, 32)
             f = int(rng.integers(96, k - 32 + 1))
@@ -305,60 +315,32 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
         qn = len(logical)
         seqs.append(SeqRows(batch=b, k_end=k, rows=np.arange(row, row + qn), n_imp=min(qn, 32)))
         row += qn
-    Q = row
-    slots = torch.from_numpy(np.concatenate(slot_list)).to(dev)
-    x = bf(Q, D)
-    w = [bf(D, D, std=0.02) for _ in range(3)]
-    ang = np.outer(np.arange(1536, dtype=np.float32),
-                   1.0 / (THETA ** (np.arange(0, HD, 2, dtype=np.float32) / HD)))
-    ang = np.concatenate([ang, ang], 1)
-    sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to(dev)
-    cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to(dev)
-    # RoPE at each row's logical position in its sequence
-    rope_row = torch.from_numpy(np.concatenate(logical_list).astype(np.int64)).to(dev)
-    kc = bf(n_slots, D)
-    vc = bf(n_slots, D)
-    q = torch.empty((Q, D), dtype=torch.bfloat16, device=dev)
-    att = torch.empty_like(q)
-    imp = torch.zeros((H, n_slots), dtype=torch.float32, device=dev)
-    plan = make_plan(seqs, table, 5, device=dev)
-    plan.validate(Q, n_slots)
-    t_qkv = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
-                                                rope_row=rope_row), reps)
-    t_att = _time_op(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
-                                                 lib.IMP_RAW_LOGIT, imp), reps)
-    qk = np.array([len(sq.rows) for sq in seqs], dtype=np.float64)
-    kk = k_ends.astype(np.float64)
-    f_att = float((4.0 * qk * kk * D).sum())
-    b_att = float((2.0 * qk * D * 2 + 2.0 * kk * D * 2).sum())
-    f_qkv = 2.0 * Q * D * 3 * D
-    out["block_table_stress"] = {
-        "workload": f"{NB} sequences, caches 512-1536 keys in permuted 32-slot pages, "
-                    f"{int(full.sum())} full recomputes, {Q} query rows, raw-logit importance",
-        "qkv_rope_cache": {"us": round(t_qkv, 2), "TFLOP/s": round(f_qkv / t_qkv / 1e6, 1),
-                           "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
-        "block_attention": {"us": round(t_att, 2), "TFLOP/s": round(f_att / t_att / 1e6, 1),
-                            "GB/s": round(b_att / t_att / 1e3, 1)},
-    }
-    # full-recompute tiles alone (the MFMA-bound class)
-    fseqs = [sq for sq in seqs if len(sq.rows) == sq.k_end]
-    if fseqs:
-        fplan = make_plan(fseqs, table, 5, device=dev)
-        t_full = _time_op(lambda: ops.block_attention(q, kc, vc, fplan, att, H, scale), reps)
-        ff = float(sum(4.0 * sq.k_end * sq.k_end * D for sq in fseqs))
-        out["block_table_stress"]["full_recompute_attention"] = {
-            "sequences": len(fseqs), "us": round(t_full, 2),
-            "TFLOP/s": round(ff / t_full / 1e6, 1),
-            "mfma_frac": round(ff / t_full / 1e6 / PEAK_BF16_TFLOPS, 4)}
+    n_slots = n_pages * P
+    x = torch.randn((row, D), generator=gen).to(torch.bfloat16)
+    w = [(torch.randn((D, D), generator=gen) * 0.02).to(torch.bfloat16) for _ in range(3)]
+    kc = torch.randn((n_slots, D), generator=gen).to(torch.bfloat16)
+    vc = torch.randn((n_slots, D), generator=gen).to(torch.bfloat16)
+    sin, cos = _rope_tables(1536)
+    return dict(NB=NB, P=P, k_ends=k_ends, full=full, table=table, seqs=seqs, Q=row,
+                n_slots=n_slots, slots=np.concatenate(slot_list).astype(np.int64),
+                rope_row=np.concatenate(logical_list).astype(np.int64), x=x, w=w, kc=kc, vc=vc,
+                sin=sin, cos=cos)
 
-    # --- Flash-Verify
+
+def build_verify(seed: int = 3) -> dict:
+    """Flash-Verify batch: 16 sequences with 1024-slot caches; k_b uniform in 4..32
+    candidates, each appended as a draft row and a [MASK] row (2 k_b rows); the cache keys
+    are the other 1024 - k_b slots; mask: no row sees its own draft (T = 0 fill rows)."""
+    import torch
+    from fdl.generate import verify_mask
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed + 100)
     NV, LC, BMV = 16, 1024, 32
-    kv = rng.integers(4, 33, NV)
-    rows = 2 * BMV  # mask rows per verify block
+    kv = np.minimum(rng.integers(4, 33, NV), BMV)
     key_pos, vblocks, masks, qslots = [], [], [], []
     k0 = q0 = 0
     for b in range(NV):
-        S = int(min(kv[b], BMV))
+        S = int(kv[b])
         cand = b * LC + 512 + np.arange(S)
         keys = np.setdiff1d(b * LC + np.arange(LC), cand)
         key_pos.append(keys)
@@ -367,26 +349,124 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
         q0 += 2 * S
         masks.append(verify_mask(0, S, BMV))
         qslots.append(np.concatenate([cand, cand]))  # draft rows, then mask rows
-    QV = q0
-    xv = bf(QV, D)
-    kcv, vcv = bf(NV * LC, D), bf(NV * LC, D)
-    sinv = torch.from_numpy(np.tile(np.sin(ang[:LC]), (NV, 1)).astype(np.float32)).to(dev)
-    cosv = torch.from_numpy(np.tile(np.cos(ang[:LC]), (NV, 1)).astype(np.float32)).to(dev)
+    x = torch.randn((q0, D), generator=gen).to(torch.bfloat16)
+    w = [(torch.randn((D, D), generator=gen) * 0.02).to(torch.bfloat16) for _ in range(3)]
+    kc = torch.randn((NV * LC, D), generator=gen).to(torch.bfloat16)
+    vc = torch.randn((NV * LC, D), generator=gen).to(torch.bfloat16)
+    sin, cos = _rope_tables(LC)
+    return dict(NV=NV, LC=LC, BMV=BMV, kv=kv, Q=q0, key_pos=np.concatenate(key_pos).astype(np.int64),
+                vblocks=np.array(vblocks, np.int32), mask=np.concatenate(masks).astype(np.uint8),
+                slots=np.concatenate(qslots).astype(np.int64), x=x, w=w, kc=kc, vc=vc,
+                sin=sin.repeat(NV, 1), cos=cos.repeat(NV, 1))
+
+
+def run_configs(reps: int = 10) -> dict:
+    """Secondary measurements on the other single-layer workloads (bf16, d_model 4096, 32
+    heads): the one-sequence 40-row layer (weight-streaming projection: HBM-bound), the
+    block-table stress batch, its full-recompute tiles on their own, and the Flash-Verify
+    batch. Synthetic N(0,1) activations and N(0,0.02) weights."""
+    import torch
+    from fdl import lib, ops
+    from fdl.schedule import SeqRows, contiguous_page_table, make_plan
+
+    dev = torch.device("cuda:0")
+    scale = 1.0 / np.sqrt(HD)
+    out = {}
+
+    # --- one sequence, 40 rows over a 384-slot cache
+    c1 = build_one_sequence()
+    w = [t.to(dev) for t in c1["w"]]
+    sin, cos = c1["sin"].to(dev), c1["cos"].to(dev)
+    kc = torch.zeros((c1["L"], D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qp = torch.empty((c1["L"], D), dtype=torch.bfloat16, device=dev)
+    ops.qkv_rope_cache(c1["x_pre"].to(dev), *w, sin, cos, torch.arange(c1["L"], device=dev), qp,
+                       kc, vc, H)
+    x = c1["x"].to(dev)
+    slot = torch.from_numpy(c1["slots"]).to(dev)
+    Q1 = x.shape[0]
+    q = torch.empty((Q1, D), dtype=torch.bfloat16, device=dev)
+    att = torch.empty_like(q)
+    plan1 = make_plan([SeqRows(batch=0, k_end=c1["L"], rows=np.arange(Q1))],
+                      contiguous_page_table(1, c1["L"]), device=dev)
+    t_q1 = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slot, q, kc, vc, H), 3 * reps)
+    t_a1 = _time_op(lambda: ops.block_attention(q, kc, vc, plan1, att, H, scale), 3 * reps)
+    b_q1 = 3.0 * D * D * 2 + Q1 * D * 2 * 4 + Q1 * HD * 4 * 2 + Q1 * 8
+    b_a1 = 2.0 * Q1 * D * 2 + 2.0 * c1["L"] * D * 2
+    out["one_sequence_40_rows"] = {
+        "workload": "1 sequence, 384-slot cache, 32-row masked block + 8 tracked rows",
+        "qkv_rope_cache": {"us": round(t_q1, 2), "GB/s": round(b_q1 / t_q1 / 1e3, 1),
+                           "hbm_frac": round(b_q1 / t_q1 / 1e3 / PEAK_HBM_GBS, 4)},
+        "block_attention": {"us": round(t_a1, 2), "GB/s": round(b_a1 / t_a1 / 1e3, 1)},
+    }
+    del kc, vc, qp
+
+    # --- block-table stress
+    st = build_stress()
+    Q = st["Q"]
+    x = st["x"].to(dev)
+    w = [t.to(dev) for t in st["w"]]
+    sin, cos = st["sin"].to(dev), st["cos"].to(dev)
+    slots = torch.from_numpy(st["slots"]).to(dev)
+    rope_row = torch.from_numpy(st["rope_row"]).to(dev)
+    kc, vc = st["kc"].to(dev), st["vc"].to(dev)
+    q = torch.empty((Q, D), dtype=torch.bfloat16, device=dev)
+    att = torch.empty_like(q)
+    imp = torch.zeros((H, st["n_slots"]), dtype=torch.float32, device=dev)
+    plan = make_plan(st["seqs"], st["table"], 5, device=dev)
+    plan.validate(Q, st["n_slots"])
+    t_qkv = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
+                                                rope_row=rope_row), reps)
+    t_att = _time_op(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
+                                                 lib.IMP_RAW_LOGIT, imp), reps)
+    qk = np.array([len(sq.rows) for sq in st["seqs"]], dtype=np.float64)
+    kk = st["k_ends"].astype(np.float64)
+    f_att = float((4.0 * qk * kk * D).sum())
+    b_att = float((2.0 * qk * D * 2 + 2.0 * kk * D * 2).sum())
+    f_qkv = 2.0 * Q * D * 3 * D
+    out["block_table_stress"] = {
+        "workload": f"{st['NB']} sequences, caches 512-1536 keys in permuted 32-slot pages, "
+                    f"{int(st['full'].sum())} full recomputes, {Q} query rows, raw-logit importance",
+        "qkv_rope_cache": {"us": round(t_qkv, 2), "TFLOP/s": round(f_qkv / t_qkv / 1e6, 1),
+                           "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
+        "block_attention": {"us": round(t_att, 2), "TFLOP/s": round(f_att / t_att / 1e6, 1),
+                            "GB/s": round(b_att / t_att / 1e3, 1)},
+    }
+    fseqs = [sq for sq in st["seqs"] if len(sq.rows) == sq.k_end]
+    if fseqs:
+        fplan = make_plan(fseqs, st["table"], 5, device=dev)
+        t_full = _time_op(lambda: ops.block_attention(q, kc, vc, fplan, att, H, scale), reps)
+        ff = float(sum(4.0 * sq.k_end * sq.k_end * D for sq in fseqs))
+        out["block_table_stress"]["full_recompute_attention"] = {
+            "sequences": len(fseqs), "us": round(t_full, 2),
+            "TFLOP/s": round(ff / t_full / 1e6, 1),
+            "mfma_frac": round(ff / t_full / 1e6 / PEAK_BF16_TFLOPS, 4)}
+    del kc, vc, imp
+
+    # --- Flash-Verify
+    vf = build_verify()
+    QV = vf["Q"]
+    xv = vf["x"].to(dev)
+    w = [t.to(dev) for t in vf["w"]]
+    kcv, vcv = vf["kc"].to(dev), vf["vc"].to(dev)
+    sinv, cosv = vf["sin"].to(dev), vf["cos"].to(dev)
     qv, k1, v1 = (torch.empty((QV, D), dtype=torch.bfloat16, device=dev) for _ in range(3))
     attv = torch.empty_like(qv)
-    kp = torch.from_numpy(np.concatenate(key_pos).astype(np.int64)).to(dev)
-    vb = torch.from_numpy(np.array(vblocks, dtype=np.int32)).to(dev)
-    mk = torch.from_numpy(np.concatenate(masks).astype(np.uint8)).to(dev)
-    qs = torch.from_numpy(np.concatenate(qslots).astype(np.int64)).to(dev)
+    kp = torch.from_numpy(vf["key_pos"]).to(dev)
+    vb = torch.from_numpy(vf["vblocks"]).to(dev)
+    mk = torch.from_numpy(vf["mask"]).to(dev)
+    qs = torch.from_numpy(vf["slots"]).to(dev)
+    rows = 2 * vf["BMV"]
     t_vq = _time_op(lambda: ops.qkv_rope_cache(xv, *w, sinv, cosv, qs, qv, k1, v1, H,
                                                kv_packed=True), reps)
     t_va = _time_op(lambda: ops.verify_attention(qv, k1, v1, kcv, vcv, kp, vb, mk, rows, attv, H,
                                                  scale), reps)
-    sk = np.minimum(kv, BMV).astype(np.float64)
+    sk = vf["kv"].astype(np.float64)
+    LC = vf["LC"]
     f_va = float((4.0 * (2 * sk) * (LC - sk + 2 * sk) * D).sum())
     b_va = float((2.0 * (LC - sk) * D * 2 + (LC - sk) * 8 + 2 * (2 * sk) * D * 2).sum())
     out["flash_verify"] = {
-        "workload": f"{NV} sequences, 1024-slot caches, {int(sk.sum())} candidates as draft "
+        "workload": f"{vf['NV']} sequences, 1024-slot caches, {int(sk.sum())} candidates as draft "
                     f"and mask rows ({QV} packed rows)",
         "qkv_rope_cache_packed": {"us": round(t_vq, 2)},
         "verify_attention": {"us": round(t_va, 2), "GB/s": round(b_va / t_va / 1e3, 1),
@@ -396,23 +476,53 @@ def run_configs(seed: int = 3, reps: int = 10) -> dict:
     return out
 
 
-def run_cpu_baseline(budget_s: float = 15.0, seed: int = 2) -> dict:
-    """Times the numpy oracle (one layer of the same workload) on the host cores."""
-    from oracle import flash_cache_oracle as orc
+def cpu_model_name() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _threads() -> int:
     try:
         from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
-        threads = os.cpu_count() or 1
-    host, _ = build_workload(seed, None)
+        return os.cpu_count() or 1
+
+
+def _median_time(fn, n: int, budget_s: float) -> tuple[float, int]:
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+        if len(times) >= n or time.perf_counter() - t_start > budget_s:
+            return float(np.median(times)), len(times)
+
+
+def run_cpu_baseline(budget_s: float = 15.0, seed: int = 2) -> dict:
+    """The numpy oracle (the reference algorithm restated on the CPU) timed on the host cores
+    for each single-layer workload: the main one (batch 8, 768 keys, 512 rows, softmax
+    importance, top-32) and, under "configs", the one-sequence 40-row layer (float32, as the
+    reference's plumbing case), the block-table stress batch and the Flash-Verify batch."""
+    from oracle import flash_cache_oracle as orc
+    threads = _threads()
     f32 = lambda t: t.float().numpy()  # noqa: E731
+    scale = 1.0 / np.sqrt(HD)
+
+    # main workload
+    host, _ = build_workload(seed, None)
     x, wq, wk, wv = f32(host["x"]), f32(host["wq"]), f32(host["wk"]), f32(host["wv"])
     kc = np.zeros((B * L, D), np.float32)
     vc = np.zeros((B * L, D), np.float32)
     pre = np.concatenate([b * L + np.arange(K_END) for b in range(B)])
     _, kc, vc = orc.qkv_proj_cache(f32(host["x_prefill"]), wq, wk, wv, host["sin"], host["cos"],
                                    pre, H, kc, vc)
-    scale = 1.0 / np.sqrt(HD)
     blocks = np.concatenate([host["mb"], host["tb"]])
 
     def one_layer():
@@ -423,30 +533,87 @@ def run_cpu_baseline(budget_s: float = 15.0, seed: int = 2) -> dict:
         for b, f in enumerate(host["frontier"]):
             orc.topk(sc, b * L + np.arange(int(f)), TOPK)
 
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t = time.perf_counter()
-        one_layer()
-        times.append(time.perf_counter() - t)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
-            break
-    return {"value": float(np.median(times) * 1e6), "unit": "us/layer", "cores": int(threads),
+    t_main, n_main = _median_time(one_layer, 5, budget_s)
+    cfg = {}
+
+    # one sequence, 40 rows, float32
+    c1 = build_one_sequence()
+    w1 = [f32(t) for t in c1["w"]]
+    s1, co1 = c1["sin"].numpy(), c1["cos"].numpy()
+    Lc = c1["L"]
+    _, kc1, vc1 = orc.qkv_proj_cache(f32(c1["x_pre"]), *w1, s1, co1, np.arange(Lc), H,
+                                     np.zeros((Lc, D), np.float32), np.zeros((Lc, D), np.float32))
+    x1 = f32(c1["x"])
+
+    def one_seq():
+        q, k2, v2 = orc.qkv_proj_cache(x1, *w1, s1, co1, c1["slots"], H, kc1, vc1)
+        orc.attend(q, k2, v2, H, scale)
+
+    t1, n1 = _median_time(one_seq, 5, budget_s / 4)
+    cfg["one_sequence_40_rows"] = {"us": round(t1 * 1e6, 1), "runs": n1,
+                                   "what": "float32 projection + RoPE + cache write, attention"}
+
+    # block-table stress
+    st = build_stress()
+    ws = [f32(t) for t in st["w"]]
+    xs, kcs, vcs = f32(st["x"]), f32(st["kc"]), f32(st["vc"])
+    ss, cs = st["sin"].numpy(), st["cos"].numpy()
+
+    def stress():
+        q, k2, v2 = orc.qkv_proj_cache(xs, *ws, ss, cs, st["slots"], H, kcs, vcs,
+                                       rope_row=st["rope_row"])
+        for sq in st["seqs"]:
+            keys = orc.key_slots(sq.batch, sq.k_end, 0, st["table"], st["P"])
+            orc.attend(q[sq.rows], k2[keys], v2[keys], H, scale)
+
+    t3, n3 = _median_time(stress, 3, budget_s / 2)
+    cfg["block_table_stress"] = {"us": round(t3 * 1e6, 1), "runs": n3,
+                                 "what": "projection + RoPE + paged cache write, attention"}
+
+    # Flash-Verify
+    vf = build_verify()
+    wv_ = [f32(t) for t in vf["w"]]
+    xv, kcv, vcv = f32(vf["x"]), f32(vf["kc"]), f32(vf["vc"])
+    sv, cv = vf["sin"].numpy(), vf["cos"].numpy()
+
+    def verify():
+        q, k1, v1 = orc.qkv_proj_cache(xv, *wv_, sv, cv, vf["slots"], H, None, None)
+        orc.verify_attention(q, k1, v1, kcv, vcv, vf["key_pos"], vf["mask"].astype(bool),
+                             vf["vblocks"], 2 * vf["BMV"], H, scale)
+
+    t4, n4 = _median_time(verify, 3, budget_s / 2)
+    cfg["flash_verify"] = {"us": round(t4 * 1e6, 1), "runs": n4,
+                           "what": "packed projection + RoPE, verify attention"}
+    return {"value": round(t_main * 1e6, 1), "unit": "us/layer", "cores": int(threads),
             "kind": "port",
-            "sample": f"numpy oracle, {len(times)} full layer(s) of the same workload "
+            "sample": f"numpy oracle, {n_main} full layer(s) of the same workload "
                       f"(QKV+RoPE+cache write, attention, softmax importance, top-32), median; "
-                      f"host os.cpu_count()={os.cpu_count()}"}
+                      f"host os.cpu_count()={os.cpu_count()}",
+            "cpu_model": cpu_model_name(), "configs": cfg}
 
 
 E2E = dict(batch=8, prompt=256, gen=512, block=32, track_num=1, mask_num=1, threshold=0.9,
            gamma=0.9, verify=True)
 
 
-def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0) -> dict:
+def _window(st, first: int, last: int) -> dict:
+    """tokens/s over steps [first, last) of a decode (steady state: after the full-recompute
+    step 0)."""
+    last = min(last, st.steps)
+    tok = float(sum(st.per_step_decoded[first:last]))
+    sec = float(sum(st.per_step_s[first:last]))
+    return {"tokens_per_s": round(tok / sec, 2) if sec > 0 else None, "steps": last - first,
+            "tokens": int(tok), "ms_per_step": round(1e3 * sec / max(last - first, 1), 3)}
+
+
+def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bool = True) -> dict:
     """Random-init LLaDA-8B (32 layers, d_model 4096, SiLU-gated MLP 12288, vocab 126464,
     bf16) under the Flash-Cache + Flash-Verify decode loop: batch 8, 256-token random
     prompts, 512 generated tokens, block 32, 32 tracked tokens, verify eps = gamma = 0.9.
-    tokens/s = decoded tokens / wall seconds of the decode loop (GPU-synchronised)."""
+    tokens/s = decoded tokens / wall seconds of the decode loop (GPU-synchronised). The HIP
+    driver and the unfused PyTorch driver are also compared over the same steady-state
+    steps 1 .. torch_steps - 1 of the same decode; with cpu_step, one steady-state step of
+    the PyTorch driver runs on the host cores (run_cpu_e2e_step)."""
     import torch
     from flash_cache_hip import flash_fused_elastic_cache
     from fdl.generate import DecodeStats, generate_with_Flash_dLLM
@@ -486,17 +653,113 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0) -> dict:
     out["paged_pool"] = {"tokens_per_s": stp.decoded / stp.wall_s, "steps": stp.steps,
                          "ms_per_step": round(1e3 * stp.wall_s / max(stp.steps, 1), 3),
                          "kv_pages": n * stride // 32}
-    if torch_steps > 0:
+    if torch_steps > 1:
+        hip_w = _window(st, 1, torch_steps)
         model.set_attention(flash_fused_elastic_cache_torch)
         stt = decode(torch_steps)
         model.set_attention(flash_fused_elastic_cache)
-        out["torch_gpu"] = {"tokens_per_s": stt.decoded / stt.wall_s, "steps": stt.steps,
-                            "ms_per_step": round(1e3 * stt.wall_s / max(stt.steps, 1), 3),
-                            "sample": f"first {stt.steps} steps (incl. the full-recompute step 0) "
-                                      "of the same decode with the unfused PyTorch driver"}
+        t_w = _window(stt, 1, torch_steps)
+        out["steady_state"] = {
+            "sample": f"steps 1..{torch_steps - 1} of the same decode (after the full-recompute "
+                      "step 0), both drivers",
+            "hip": hip_w, "torch_gpu": t_w,
+            "speedup": round(hip_w["tokens_per_s"] / t_w["tokens_per_s"], 2)
+            if hip_w["tokens_per_s"] and t_w["tokens_per_s"] else None}
+        out["torch_gpu"] = {"tokens_per_s": t_w["tokens_per_s"], "steps": t_w["steps"],
+                            "ms_per_step": t_w["ms_per_step"],
+                            "sample": "steady-state steps of the same decode with the unfused "
+                                      "PyTorch driver (every op a PyTorch op)"}
+    if cpu_step:
+        tps = _window(st, 1, st.steps)
+        per_step = tps["tokens"] / max(tps["steps"], 1)
+        out["cpu"] = run_cpu_e2e_step(model, per_step)
     del model
     torch.cuda.empty_cache()
     return out
+
+
+def run_cpu_e2e_step(model_gpu, tokens_per_step: float, seed: int = 0) -> dict:
+    """One steady-state Flash-Cache + Flash-Verify step of the same LLaDA-8B (weights copied
+    from the GPU model) with the unfused PyTorch driver on the host cores: the pass-1
+    forward over 8 x (32 masked + 32 tracked) rows against 896-slot caches (768 keys, 512
+    decoded), LM head on the 256 masked rows, then the verify forward over 8 x 64 rows (32
+    fill rows, 16 drafts, 16 masks) against the other 848 keys, LM head on the 128 mask
+    rows. Caches hold N(0,1) values. tokens/s = tokens per step of the GPU decode / the two
+    forwards' seconds."""
+    import torch
+    from fdl.generate import get_rotary_embedding, make_blocks, verify_mask
+    from fdl.model import LLaDAModelLM
+    from fdl.torch_path import flash_fused_elastic_cache_torch
+
+    cfg = model_gpu.config
+    bf = torch.bfloat16
+    with torch.device("meta"):
+        cpu = LLaDAModelLM(cfg, flash_fused_elastic_cache_torch, device="meta", dtype=bf)
+    cpu = cpu.to_empty(device="cpu")
+    src = model_gpu.state_dict()
+    with torch.no_grad():
+        for name, p_ in cpu.state_dict().items():
+            p_.copy_(src[name].cpu())
+    cpu.eval()
+    nb, bm, Lc, k_end, nd = E2E["batch"], E2E["block"], 896, 768, 512
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    for blk in cpu.model.transformer.blocks:
+        blk.k_cache = torch.randn((nb * Lc, cfg.d_model), generator=gen).to(bf)
+        blk.v_cache = torch.randn((nb * Lc, cfg.d_model), generator=gen).to(bf)
+    sin, cos = get_rotary_embedding(Lc, HD, cfg.rope_theta, "cpu")
+    rope = [sin.repeat(nb, 1), cos.repeat(nb, 1)]
+    scores = torch.zeros(nb * Lc, dtype=torch.float32)
+    # pass 1: masked rows of every sequence, then tracked rows
+    masked = [j * Lc + np.arange(nd, nd + bm) for j in range(nb)]
+    tracked = [j * Lc + np.sort(rng.choice(nd, bm, replace=False)) for j in range(nb)]
+    mb = np.concatenate([make_blocks(j, [k_end] * nb, bm * j, bm * (j + 1), bm) for j in range(nb)])
+    tb = np.concatenate([make_blocks(j, [k_end] * nb, nb * bm + bm * j, nb * bm + bm * (j + 1), bm)
+                         for j in range(nb)])
+    qpos = torch.from_numpy(np.concatenate(masked + tracked))
+    mb_t, tb_t = torch.from_numpy(mb), torch.from_numpy(tb)
+    ids = torch.from_numpy(rng.integers(0, 126000, len(qpos)))[None]
+    pos1 = [qpos, torch.zeros(0, dtype=torch.int32), rope, None, scores, []]
+    len1 = [[-1] * nb, None, mb_t, tb_t, torch.cat([mb_t, tb_t]), list(range(nb)), nb, Lc, bm, 128,
+            None, False]
+    # verify: T = 32 fill rows, S = 16 candidates (drafts, then masks) per sequence
+    S, T = bm // 2, bm
+    vpos, keys, vblocks, masks = [], [], [], []
+    k0 = q0 = 0
+    for j in range(nb):
+        fill = j * Lc + np.arange(nd - T, nd)
+        cand = j * Lc + np.arange(nd, nd + S)
+        vpos.append(np.concatenate([fill, cand, cand]))
+        kj = np.concatenate([j * Lc + np.arange(nd - T), j * Lc + np.arange(nd + S, Lc)])
+        keys.append(kj)
+        vblocks.append((k0, k0 + len(kj), q0, q0 + 2 * bm))
+        k0 += len(kj)
+        q0 += 2 * bm
+        masks.append(verify_mask(T, S, bm))
+    vq = torch.from_numpy(np.concatenate(vpos))
+    pos2 = [vq, torch.from_numpy(np.concatenate(keys)), rope, None, scores,
+            torch.from_numpy(np.concatenate(masks))]
+    len2 = [[-1] * nb, torch.tensor(vblocks, dtype=torch.int32), None, tb_t, None, list(range(nb)),
+            nb, Lc, bm, 128, None, True]
+    vids = torch.from_numpy(rng.integers(0, 126000, len(vq)))[None]
+    rows1 = torch.arange(nb * bm)
+    rows2 = torch.cat([torch.arange(j * 2 * bm + T + S, j * 2 * bm + T + 2 * S) for j in range(nb)])
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        cpu(ids, use_cache=True, lengths=len1, positions=pos1, logit_rows=rows1)
+        t1 = time.perf_counter()
+        cpu(vids, use_cache=True, lengths=len2, positions=pos2, logit_rows=rows2)
+        t2 = time.perf_counter()
+    sec = t2 - t0
+    del cpu
+    return {"tokens_per_s": round(tokens_per_step / sec, 4), "unit": "tokens/s",
+            "seconds_per_step": round(sec, 2), "pass1_s": round(t1 - t0, 2),
+            "verify_s": round(t2 - t1, 2), "tokens_per_step": round(tokens_per_step, 3),
+            "cores": torch.get_num_threads(), "cpu_model": cpu_model_name(), "kind": "port",
+            "sample": "one steady-state step (pass-1 forward, 512 rows; verify forward, 512 rows) "
+                      "of the unfused PyTorch driver in bf16 on the host cores, LLaDA-8B weights "
+                      "copied from the GPU model, caches N(0,1); tokens per step from the GPU "
+                      "decode's steady state"}
 
 
 def main() -> int:
@@ -583,9 +846,13 @@ def main() -> int:
     if not args.no_configs:
         out["configs"] = run_configs()
     if not args.no_e2e:
-        out["e2e_llada8b"] = run_e2e(args.e2e_steps, args.e2e_torch_steps)
+        out["e2e_llada8b"] = run_e2e(args.e2e_steps, args.e2e_torch_steps,
+                                     cpu_step=not args.no_cpu)
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(args.cpu_budget)
+        cpu_e2e = out.get("e2e_llada8b", {}).get("cpu")
+        if cpu_e2e:
+            out["cpu_baseline"]["configs"]["e2e_llada8b"] = cpu_e2e
     print(json.dumps(out), flush=True)
     return 0
 

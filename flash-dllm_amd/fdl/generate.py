@@ -103,6 +103,7 @@ class DecodeStats:
     split_rank_steps: int = 0  # steps that reduced first (a ranked row without importance)
     wall_s: float = 0.0
     per_step_s: list = field(default_factory=list)
+    per_step_decoded: list = field(default_factory=list)  # tokens decoded in each step
 
 
 class _Seq:
@@ -624,6 +625,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 start_layer[j] = n_layers
         stats.steps += 1
         stats.per_step_s.append(time.perf_counter() - t_step)
+        stats.per_step_decoded.append(stats.decoded - sum(stats.per_step_decoded))
         if all(a == -1 for a in active) and count >= len(prompts):
             break
         if max_steps is not None and stats.steps >= max_steps:

@@ -4,9 +4,11 @@ measured against on the same GPU (and a second implementation for end-to-end cro
 Same contract as flash_cache_hip.flash_fused_elastic_cache (flash_cache_triton.py:462-638):
 F.linear Q/K/V, rotate-half RoPE on gathered sin/cos rows, index_copy_ into the caches,
 per-block softmax attention in float32 (probabilities cast to bf16 before PV, like
-flash_cache_triton.py:168), the raw-logit importance `attn_scores += S.mean((0, 1))`, and
-the verify attention over gathered cache keys plus in-block keys under the mask. It is
-selected explicitly (model.set_attention); nothing falls back to it.
+flash_cache_triton.py:168), the raw-logit importance `attn_scores += S.mean((0, 1))`, the
+verify attention over gathered cache keys plus in-block keys under the mask, and the
+block's norm/MLP tail with the model's own modules. Every op is a PyTorch op: no HIP kernel
+of this build runs here. It is selected explicitly (model.set_attention); nothing falls
+back to it.
 """
 from __future__ import annotations
 
@@ -50,10 +52,25 @@ def _attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_heads: int, sca
     return o.transpose(0, 1).reshape(rows, d).to(q.dtype), raw
 
 
+def _mlp_tail(self, x: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
+    """attn_out + residual + gated MLP + residual with plain modules, each step as the
+    reference writes it (flash_cache_triton.py:618-638)."""
+    ck = self._activation_checkpoint_fn
+    att = self.attn_out(att)
+    x = x + self.dropout(att)
+    og_x = x
+    x = ck(self.ff_norm, x) if ck is not None else self.ff_norm(x)
+    x, x_up = self.ff_proj(x), self.up_proj(x)
+    x = ck(self.act, x) if ck is not None else self.act(x)
+    x = x * x_up
+    x = self.ff_out(x)
+    x = self.dropout(x)
+    x = og_x + x
+    return x.unsqueeze(0)
+
+
 def flash_fused_elastic_cache_torch(self, x: torch.Tensor, block_idx, positions, lengths,
                                     softmax_scale: float = None):
-    from flash_cache_hip import block_mlp_tail
-
     query_pos_flat, key_pos_flat, rotary_emb_pos, info, attn_scores, attn_mask = positions
     (start_layer, query_verify_blocks, query_masked_blocks, query_tracked_blocks, query_blocks,
      active_batch, num_active, max_length, block_m, block_n, elastic_cache, verify) = lengths
@@ -113,4 +130,4 @@ def flash_fused_elastic_cache_torch(self, x: torch.Tensor, block_idx, positions,
         if importance:
             attn_scores += S_mean
 
-    return block_mlp_tail(self, x, att)
+    return _mlp_tail(self, x, att)
