@@ -69,6 +69,8 @@ struct AttnArgs {
   const int32_t* vblocks;    // verify
   const uint8_t* mask;       // verify
   float* imp_part;
+  float* ws;         // softmax importance: probabilities of the importance rows (see kWsBlock)
+  int ws_blocks;     // key blocks of room per (work item, head) in ws; 0: no workspace
   int64_t n_slots;
   int64_t n_q_rows;
   int64_t n_keys;
@@ -112,6 +114,26 @@ __device__ __forceinline__ float xsum(float v) {
   const auto b =
       __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Sum over the 16 lanes of each lane group (lanes 16 g .. 16 g + 15) with DPP moves: quad
+// exchanges (lane ^ 1, lane ^ 2), then the 8-lane and the 16-lane mirror; every step adds
+// a lane pair in both orders, so all 16 lanes get the same bits.
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+  int t;
+  switch (ctrl_sel) {
+    case 0: t = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false); break;  // [1,0,3,2]
+    case 1: t = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false); break;  // [2,3,0,1]
+    case 2: t = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false); break;  // half mirror
+    default: t = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false); break;  // mirror
+  }
+  return v + __int_as_float(t);
+}
+__device__ __forceinline__ float sum16(float v) {
+  v = dpp_add(v, 0);
+  v = dpp_add(v, 1);
+  v = dpp_add(v, 2);
+  return dpp_add(v, 3);
 }
 
 // Waits until at most n global loads of this wavefront are outstanding (n a multiple of
@@ -324,36 +346,34 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
   }
 }
 
-// Softmax importance kept in LDS (kStore kernels): the probabilities of up to kStoreRows
-// importance rows over up to kStoreBlocks key blocks, as fp16, each block relative to the
-// row's reference maximum at that block; the column sums are formed once the rows'
-// log-sum-exp is known, so K is not read a second time.
+// Softmax importance in one pass: the fp32 probabilities of up to kStoreRows importance rows
+// are written, block by block, to the caller's workspace, each block relative to the row's
+// reference maximum at that block, and the column sums are formed once the rows' log-sum-exp
+// is known, so K is not read a second time. Per (work item, head) the workspace holds
+// ws_blocks records of kWsBlock floats: [row][key] probabilities, then the rows' maxima.
 constexpr int kStoreRows = 32;
-constexpr int kStoreBlocks = 12;
+constexpr int kWsBlock = kStoreRows * kTileN + kStoreRows;
 
 // Steps of a tile, the same sequence for producers and consumers (one barrier each):
 //   [0, n_blk)          cache blocks, K and V
 //   [n_blk, 2 n_blk)    softmax importance without the LDS store: the cache blocks again,
 //                       K only, last block first
 //   n_blk               verify only (when the block has rows): the in-block keys
-template <int RB, int NC, bool kVerify, bool kStore = false>
+template <int RB, int NC, bool kVerify>
 __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
   constexpr int kRows = 16 * RB * NC;
-  constexpr int kSt = kStore ? 3 : kStages;  // LDS ring depth (the store needs the room)
+  constexpr int kSt = kStages;  // LDS ring depth
   __shared__ __align__(1024) uint8_t smem[kSt * kStageBytes];
   __shared__ float imp_buf[2][NC][kTileN];  // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
-  // raw importance: sum of the importance rows' Q and its MFMA A-operand fragments, by lane
-  __shared__ float qsum_buf[kStore ? 1 : kHeadDim];
-  __shared__ u32x4 qsum_frag_buf[kStore ? 1 : 4][64];
+  // raw importance: each consumer's column sums of its importance rows' Q, and the summed Q
+  // as MFMA A-operand fragments, by lane
+  __shared__ float qsum_part[kVerify ? 1 : NC][kHeadDim];
+  __shared__ u32x4 qsum_frag_buf[kVerify ? 1 : 4][64];
   // raw importance of key k_begin + i, written to imp_part after the key loop (a consumer's
   // global store inside the loop would wait behind the producers' loads)
-  __shared__ float raw_buf[kStore || kVerify ? 1 : kSlotCache];
-  // kStore: fp16 probabilities [block][row][key] (8-byte units XOR-swizzled by row) and the
-  // rows' reference maxima [block][row]
-  __shared__ __align__(16) uint16_t prob_buf[kStore ? kStoreBlocks * kStoreRows * kTileN : 4];
-  __shared__ float pmax_buf[kStore ? kStoreBlocks * kStoreRows : 1];
+  __shared__ float raw_buf[kVerify ? 1 : kSlotCache];
 
   const int tid = threadIdx.x;
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
@@ -399,13 +419,17 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
 
-  const bool imp_raw = !kStore && !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
+  const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
   const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
   const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
   const bool inblock = kVerify && n_rows > 0;
-  // softmax importance from the LDS store (one pass) or from a second pass over K
-  const bool store = kStore && imp_soft && n_imp <= kStoreRows && n_blk <= kStoreBlocks;
+  // softmax importance from the workspace (one pass) or from a second pass over K
+  // (64-row tiles only: the 128-row variant's twelve wavefronts leave too few registers)
+  const bool store = NC == 4 && imp_soft && n_imp <= kStoreRows && n_blk <= a.ws_blocks;
   const bool two_pass = imp_soft && !store;
+  float* ws_tile = store ? a.ws + (int64_t(a.split ? blockIdx.x >> 1 : blockIdx.x) * gridDim.y +
+                                   blockIdx.y) * a.ws_blocks * kWsBlock
+                         : nullptr;
   const int n_steps = n_blk * (two_pass ? 2 : 1) + (inblock ? 1 : 0);
   // Step -> key block: the first pass walks the blocks forward, the second (softmax
   // importance, K only) walks them backward, so it starts with the last kSt blocks of the
@@ -498,6 +522,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       issue(s + kSt);
     }
     wait_vmcnt(0);  // no load may still be writing LDS when the workgroup ends
+    if (store) __syncthreads();  // the consumers' workspace stores are complete
     return;
   }
 
@@ -564,11 +589,37 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   };
 
   // Raw importance from the summed Q (qsum_fragment): one wavefront per block computes all
-  // 64 column sums.
-  if (imp_raw && tid < kHeadDim) qsum_buf[tid] = sum_q_rows(a, roff, n_imp, D, col0 + tid);
+  // 64 column sums. Each consumer first sums its importance rows' Q columns from its own Q
+  // fragments (the 16 rows of a lane group, reduced across the group's lanes).
+  if constexpr (!kVerify) {
+    if (imp_raw && wave_imp) {
+#pragma unroll
+      for (int sd = 0; sd < 4; ++sd)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float v = 0.f;
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+            if (16 * (wr * RB + rb) + l16 < n_imp) v += static_cast<float>(qf[rb][sd][j]);
+          v = sum16(v);
+          if (l16 == 0) qsum_part[wr][32 * sd + 8 * g + j] = v;
+        }
+    }
+  }
   barrier_lds_drained();  // #0
   // A-operand fragment sd of the summed Q (rows 0-2 its three bf16 parts), built by wave sd
-  if (imp_raw && wr < 4) qsum_frag_buf[wr][lane] = qsum_fragment(qsum_buf, wr, l16, g);
+  // from the consumers' partial sums, added in ascending consumer order
+  if constexpr (!kVerify) {
+    if (imp_raw && wr < 4) {
+      float* qs = qsum_part[imp_waves - 1];
+      if (lane < 32) {
+        float v = 0.f;
+        for (int w = 0; w < imp_waves; ++w) v += qsum_part[w][32 * wr + lane];
+        qs[32 * wr + lane] = v;  // the last partial's own column, read only by wave wr
+      }
+      qsum_frag_buf[wr][lane] = qsum_fragment(qs, wr, l16, g);
+    }
+  }
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
   for (int s = 0; s < n_steps; ++s) {
@@ -601,20 +652,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       attend_block<RB>(
           st, qf, kt, vt, a.scale_log2, [&](int, int kb, int ii) { return kbias[kb][ii]; },
           [&](int rb, const f32x4 (&p)[4], float m_use) {
-            if constexpr (kStore) {
-              const int r = 16 * (wr * RB + rb) + l16;
-              if (store && r < kStoreRows) {
-                // row r, keys 16 kb + 4 g .. + 3: 8-byte unit 4 kb + g, swizzled by row
-                uint16_t* prow = prob_buf + (blk * kStoreRows + r) * kTileN;
+            const int r = 16 * (wr * RB + rb) + l16;
+            if (store && r < kStoreRows) {
+              // row r, keys 16 kb + 4 g .. + 3 of block blk; then the row's maximum
+              float* rec = ws_tile + int64_t(blk) * kWsBlock;
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                  u32x2 w;
-                  w[0] = pack_f16x2(p[kb][0], p[kb][1]);
-                  w[1] = pack_f16x2(p[kb][2], p[kb][3]);
-                  st8(prow + 4 * ((4 * kb + g) ^ ((r >> 1) & 15)), w);
-                }
-                if (g == 0) pmax_buf[blk * kStoreRows + r] = m_use;
-              }
+              for (int kb = 0; kb < 4; ++kb)
+                *reinterpret_cast<f32x4*>(rec + r * kTileN + 16 * kb + 4 * g) = p[kb];
+              if (g == 0) rec[kStoreRows * kTileN + r] = m_use;
             }
           });
       if (imp_raw && wr < 4) {
@@ -626,7 +671,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         const int n = n0 + 16 * wr + l16;
         if (g == 0 && n < k_end) {
           const float v = qsum_dot(acc);
-          if constexpr (!kStore && !kVerify) {
+          if constexpr (!kVerify) {
             if (slots_staged) raw_buf[n - k_begin] = v;
             else imp_out[slot_of(n)] = v;
           }
@@ -667,25 +712,48 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     barrier_lds_drained();  // step s consumed; step s + 1 landed
   }
   if (two_pass && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
-  if constexpr (!kStore && !kVerify) {
+  // the output first: its accumulators are then free for the importance epilogue
+  if (!l_reduced) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+  }
+  write_out();
+  if constexpr (!kVerify) {
     if (imp_raw && slots_staged) {
       // the last step's barrier made every block's sums visible
       for (int i = tid; i < k_end - k_begin; i += 64 * NC) imp_out[slot_buf[i]] = raw_buf[i];
     }
-  }
-  if constexpr (kStore) {
-    if (store) {
-      // every block's probabilities, maxima and the rows' log-sum-exp are in LDS (the last
-      // step's barrier); column sums over the importance rows in ascending row order
+    if (NC == 4 && store) {
+      // every block's probabilities and maxima are in the workspace once every consumer's
+      // stores have completed (the barrier's release), the rows' log-sum-exp in LDS; column
+      // sums over the importance rows in ascending row order
+      wait_vmcnt(0);
+      __syncthreads();
       const int nk = k_end - k_begin;
       for (int k0 = 4 * tid; k0 < nk; k0 += 4 * 64 * NC) {
-        const int j = k0 / kTileN, u = (k0 % kTileN) / 4;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int r = 0; r < n_imp; ++r) {
-          const float c = fast_exp2(pmax_buf[j * kStoreRows + r] - lse_buf[r]);
-          const u32x2 w = ld8(prob_buf + (j * kStoreRows + r) * kTileN + 4 * (u ^ ((r >> 1) & 15)));
+        const int j = k0 / kTileN, u = k0 % kTileN;
+        const float* rec = ws_tile + int64_t(j) * kWsBlock;
+        // every row's probabilities and maximum are loaded before the first is used, so the
+        // loads are in flight together (the callback above writes all kStoreRows rows of a
+        // record, finite; rows past n_imp are dropped by the select)
+        constexpr int kChunk = kStoreRows;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[e] += c * f16_bits_to_f32(w[e >> 1], e & 1);
+        for (int r0 = 0; r0 < kStoreRows; r0 += kChunk) {
+          f32x4 pv[kChunk], mx[kChunk / 4];
+#pragma unroll
+          for (int i = 0; i < kChunk; ++i)
+            pv[i] = *reinterpret_cast<const f32x4*>(rec + (r0 + i) * kTileN + u);
+#pragma unroll
+          for (int i4 = 0; i4 < kChunk / 4; ++i4)
+            mx[i4] = *reinterpret_cast<const f32x4*>(rec + kStoreRows * kTileN + r0 + 4 * i4);
+#pragma unroll
+          for (int i = 0; i < kChunk; ++i) {
+            const int r = r0 + i;
+            const float c = fast_exp2(mx[i / 4][i % 4] - lse_buf[r]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = r < n_imp ? acc[e] + c * pv[i][e] : acc[e];
+          }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -695,11 +763,6 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       }
     }
   }
-  if (!l_reduced) {
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
-  }
-  write_out();
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1186,9 +1249,9 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
-template <int RB, int NC, bool kVerify, bool kStore = false>
+template <int RB, int NC, bool kVerify>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify, kStore>),
+  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>),
                      dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
                      dim3(64 * (NC + kProducers)), 0, s, args);
   return hipGetLastError();
@@ -1210,7 +1273,8 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
                            int64_t max_pages, int32_t page_log2, const int32_t* work,
                            int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
                            int32_t tile_rows, float softmax_scale, void* out, int32_t imp_mode,
-                           float* imp_part, hipStream_t s) {
+                           float* imp_part, float* workspace, int64_t workspace_floats,
+                           hipStream_t s) {
   int rc = check_common(fn, q, k_cache, v_cache, out, d_model, n_heads, head_dim);
   if (rc != FDL_OK) return rc;
   FDL_REQUIRE_ARG(page_table);
@@ -1237,6 +1301,17 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
   args.n_row_idx = n_row_idx;
   args.n_seq = static_cast<int>(n_seq);
   args.imp_part = imp_part;
+  FDL_REQUIRE(workspace_floats >= 0 && (workspace_floats == 0 || workspace != nullptr),
+              FDL_ERR_NULL, "%s: workspace is NULL with workspace_floats = %lld", fn,
+              (long long)workspace_floats);
+  if (imp_mode == FDL_IMP_SOFTMAX_COLSUM && workspace != nullptr) {
+    FDL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, FDL_ERR_SHAPE,
+                "%s: workspace must be 16-byte aligned", fn);
+    // room per (work item, head), in key blocks (tiles beyond it take the second pass)
+    const int64_t per = workspace_floats / (n_work * n_heads * kWsBlock);
+    args.ws = workspace;
+    args.ws_blocks = static_cast<int>(per < (int64_t(1) << 30) ? per : (int64_t(1) << 30));
+  }
   args.n_slots = n_slots;
   args.n_q_rows = n_q_rows;
   args.max_pages = static_cast<int>(max_pages);
@@ -1335,7 +1410,8 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
                                    int32_t page_log2, const int32_t* work, int64_t n_work,
                                    const int32_t* row_idx, int64_t n_row_idx, int32_t tile_rows,
                                    float softmax_scale, void* out, int32_t imp_mode,
-                                   float* imp_part, void* stream) {
+                                   float* imp_part, float* workspace, int64_t workspace_floats,
+                                   void* stream) {
   using namespace fdl;
   FDL_REQUIRE(n_work >= 0 && n_work < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_block_attention: n_work = %lld out of range", (long long)n_work);
@@ -1345,7 +1421,8 @@ extern "C" int fdl_block_attention(const void* q, const void* k_cache, const voi
   const int rc = block_attention_launch("fdl_block_attention", q, k_cache, v_cache, n_q_rows, n_slots, d_model, n_heads,
                                         head_dim, page_table, n_seq, max_pages, page_log2, work,
                                         n_work, row_idx, n_row_idx, tile_rows, softmax_scale, out,
-                                        imp_mode, imp_part, static_cast<hipStream_t>(stream));
+                                        imp_mode, imp_part, workspace, workspace_floats,
+                                        static_cast<hipStream_t>(stream));
   return rc == FDL_OK ? ok() : rc;
 }
 
@@ -1380,11 +1457,20 @@ extern "C" int fdl_block_attention_scores_noalloc(
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // every partial the reduction reads is written by the attention first (the keys of the
   // importance tiles), so the scratch needs no clearing between calls
+  // the scratch holds the partials [n_heads][n_slots], then (16-byte aligned) the softmax
+  // importance workspace in what is left
+  float* ws = nullptr;
+  int64_t ws_floats = 0;
+  if (imp_mode == FDL_IMP_SOFTMAX_COLSUM) {
+    const int64_t off = (n_heads * n_slots + 3) / 4 * 4;
+    ws = part + off;
+    ws_floats = kScratchFloats - off;
+  }
   int rc = block_attention_launch("fdl_block_attention_scores_noalloc", q, k_cache, v_cache,
                                   n_q_rows, n_slots, d_model, n_heads,
                                   head_dim, page_table, n_seq, max_pages, page_log2, work, n_work,
                                   row_idx, n_row_idx, tile_rows, softmax_scale, out, imp_mode,
-                                  part, s);
+                                  part, ws, ws_floats, s);
   if (rc == FDL_OK && imp_mode != FDL_IMP_NONE)
     rc = importance_accumulate_launch("fdl_block_attention_scores_noalloc", part, n_heads, n_slots, page_table, n_seq, max_pages,
                                       page_log2, work, n_work, imp_scale, scores, s);

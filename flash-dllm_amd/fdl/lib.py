@@ -24,6 +24,10 @@ FDL_ERR_RANGE = -3
 FDL_ERR_UNSUPPORTED = -4
 FDL_ERR_HIP = -5
 
+ABI_VERSION = 2  # FDL_ABI_VERSION of include/fdl.h
+# fp32 workspace per 64-key block, head and tile of softmax importance (FDL_ATTN_WS_FLOATS_PER_BLOCK)
+ATTN_WS_FLOATS_PER_BLOCK = 32 * 64 + 32
+
 IMP_NONE = 0
 IMP_RAW_LOGIT = 1
 IMP_SOFTMAX_COLSUM = 2
@@ -68,6 +72,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _i64, _i64, _i32,         # page_table, n_seq, max_pages, page_log2
         _p, _i64, _p, _i64, _i32,     # work, n_work, row_idx, n_row_idx, tile_rows
         _f32, _p, _i32, _p,           # softmax_scale, out, imp_mode, imp_part
+        _p, _i64,                     # workspace, workspace_floats
         _p,                           # stream
     ]),
     "fdl_block_attention_scores_noalloc": (ctypes.c_int, [
@@ -136,8 +141,9 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.fdl_abi_version() != 1:
-        raise FdlError(FDL_ERR_UNSUPPORTED, f"{path}: ABI version {lib.fdl_abi_version()} != 1")
+    if lib.fdl_abi_version() != ABI_VERSION:
+        raise FdlError(FDL_ERR_UNSUPPORTED,
+                       f"{path}: ABI version {lib.fdl_abi_version()} != {ABI_VERSION}; rebuild it")
     _lib = lib
     return lib
 

@@ -87,10 +87,35 @@ def qkv_rope_cache(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torc
               1 if kv_packed else 0, _stream(x))
 
 
+def _class_ranges(plan: AttnPlan):
+    """(first, count, tile_rows) of the plan's long, mid and short tiles."""
+    n_short = plan.n_work - plan.n_long - plan.n_mid
+    return ((0, plan.n_long, LONG_TILE_ROWS), (plan.n_long, plan.n_mid, MID_TILE_ROWS),
+            (plan.n_long + plan.n_mid, n_short, MAX_TILE_ROWS))
+
+
+def attention_workspace_floats(plan: AttnPlan, n_heads: int) -> int:
+    """fp32 workspace that lets every importance tile of the plan keep its softmax-importance
+    probabilities for one pass (fdl_block_attention's workspace; the launches of one call
+    reuse it)."""
+    need = 0
+    for first, count, _ in _class_ranges(plan):
+        if count == 0:
+            continue
+        w = plan.work[first:first + count]
+        blocks = int(((w[:, 2] - w[:, 1] + 63) // 64).max()) if (w[:, 5] > 0).any() else 0
+        need = max(need, count * n_heads * blocks * _lib.ATTN_WS_FLOATS_PER_BLOCK)
+    return need
+
+
 def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     plan: AttnPlan, out: torch.Tensor, n_heads: int, softmax_scale: float,
-                    imp_mode: int = _lib.IMP_NONE, imp_part: torch.Tensor | None = None) -> None:
-    """Block-table attention with the importance side output (fdl_block_attention)."""
+                    imp_mode: int = _lib.IMP_NONE, imp_part: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> None:
+    """Block-table attention with the importance side output (fdl_block_attention). With
+    softmax-colsum importance a float32 `workspace` of attention_workspace_floats(plan,
+    n_heads) elements keeps the importance rows' probabilities (allocated from torch's
+    caching allocator when not given)."""
     dev = q.device
     _need(q, "q", BF16, 2)
     _need(k_cache, "k_cache", BF16, 2, dev)
@@ -112,11 +137,13 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     if imp_mode == _lib.IMP_SOFTMAX_COLSUM and plan.n_long and int(plan.work[:plan.n_long, 5].max()) > MID_TILE_ROWS:
         raise _lib.FdlError(_lib.FDL_ERR_UNSUPPORTED,
                             f"softmax-colsum importance needs at most {MID_TILE_ROWS} importance rows per sequence")
+    if imp_mode == _lib.IMP_SOFTMAX_COLSUM and workspace is None:
+        workspace = torch.empty(max(attention_workspace_floats(plan, n_heads), 4),
+                                dtype=torch.float32, device=dev)
+    if workspace is not None:
+        _need(workspace, "workspace", torch.float32, 1, dev)
     # long tiles (the first n_long work items), mid tiles (the next n_mid), short tiles
-    n_short = plan.n_work - plan.n_long - plan.n_mid
-    for first, count, tile_rows in ((0, plan.n_long, LONG_TILE_ROWS),
-                                    (plan.n_long, plan.n_mid, MID_TILE_ROWS),
-                                    (plan.n_long + plan.n_mid, n_short, MAX_TILE_ROWS)):
+    for first, count, tile_rows in _class_ranges(plan):
         if count == 0:
             continue
         _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -124,7 +151,8 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                   plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
                   plan.page_log2, plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(),
                   n_row_idx, tile_rows, float(softmax_scale), out.data_ptr(), int(imp_mode),
-                  _ptr(imp_part), stream)
+                  _ptr(imp_part), _ptr(workspace), 0 if workspace is None else workspace.numel(),
+                  stream)
 
 
 def importance_accumulate(imp_part: torch.Tensor, plan: AttnPlan, scale: float,

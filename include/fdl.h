@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FDL_ABI_VERSION 1
+#define FDL_ABI_VERSION 2
 
 enum fdl_status {
   FDL_OK = 0,
@@ -110,22 +110,33 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            Slots of other tiles are left untouched. Reduce over heads with
  *            fdl_importance_accumulate. Each sequence must have at most one tile with
  *            n_imp > 0.
+ *   workspace fp32 [workspace_floats], 16-byte aligned, or NULL / 0: with
+ *            FDL_IMP_SOFTMAX_COLSUM, the importance rows' probabilities (at most 32 rows) are
+ *            kept here during the one pass over K/V; a tile needs
+ *            FDL_ATTN_WS_FLOATS_PER_BLOCK floats per 64-key block for each head, and the room
+ *            per tile is workspace_floats / (n_work * n_heads). A tile whose keys do not fit
+ *            (or with more than 32 importance rows, or without a workspace) reads K a second
+ *            time instead; the results are the same. Contents need no initialisation and are
+ *            left undefined.
  */
+#define FDL_ATTN_WS_FLOATS_PER_BLOCK (32 * 64 + 32)
 int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
                         int64_t n_q_rows, int64_t n_slots, int64_t d_model, int64_t n_heads,
                         int64_t head_dim, const int32_t* page_table, int64_t n_seq,
                         int64_t max_pages, int32_t page_log2, const int32_t* work,
                         int64_t n_work, const int32_t* row_idx, int64_t n_row_idx,
                         int32_t tile_rows, float softmax_scale, void* out, int32_t imp_mode,
-                        float* imp_part, void* stream);
+                        float* imp_part, float* workspace, int64_t workspace_floats,
+                        void* stream);
 
 /*
  * No counterpart in the reference. For callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops or harnesses that forbid hipMalloc): one call does
  * fdl_block_attention followed by fdl_importance_accumulate, with the per-head importance
- * partials in a library-owned static device array of FDL_NOALLOC_SCRATCH_BYTES (32 MiB) on
- * each GPU, held until the process ends, instead of a caller workspace. The caller still
- * passes the inputs, `out` and `scores`; nothing is allocated (no hipMalloc/hipFree).
+ * partials (and, in what is left, fdl_block_attention's softmax-importance workspace) in a
+ * library-owned static device array of FDL_NOALLOC_SCRATCH_BYTES (32 MiB) on each GPU, held
+ * until the process ends, instead of caller workspaces. The caller still passes the inputs,
+ * `out` and `scores`; nothing is allocated (no hipMalloc/hipFree).
  *   out     as fdl_block_attention
  *   scores  fp32 [n_slots], with imp_mode != FDL_IMP_NONE:
  *           scores[slot(n)] += imp_scale * sum_h (head-h importance of key n), heads summed in

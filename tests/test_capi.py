@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lib.SIGNATURES), "ctypes signatures out of sync with fdl.h"
-    assert L.fdl_abi_version() == 1
+    assert L.fdl_abi_version() == lib.ABI_VERSION
 
 
 def _expect(status, name, *args):
@@ -51,13 +51,13 @@ def test_launchers_reject_bad_scalars_without_gpu():
     lib.call("fdl_qkv_rope_cache", None, None, None, None, None, None, 0, None, None, 0,
              4096, 32, 128, None, None, None, 0, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128,
-            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None)
+            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None, 0, None)
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_block_attention", None, None, None, 4, 4, 2048, 32, 64,
-            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None)
+            None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, 0, None, None, 0, None)
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128,
-            None, 1, 1, 5, None, 1, None, 1, 96, 0.1, None, 0, None, None)
+            None, 1, 1, 5, None, 1, None, 1, 96, 0.1, None, 0, None, None, 0, None)
     lib.call("fdl_block_attention", None, None, None, 4, 4, 4096, 32, 128, None, 1, 1, 5, None,
-             0, None, 1, 64, 0.1, None, 0, None, None)
+             0, None, 1, 64, 0.1, None, 0, None, None, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_rank", None, 10, None, 10, None, 1, 16, None, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 5,
             None, None, 10, None, 10, None, 1, 16, None, 0, None)

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from fdl import lib
+from fdl import lib, ops
 from fdl.schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, MID_TILE_ROWS, SeqRows, make_plan
 
 DEV = "cuda:0"
@@ -59,6 +59,9 @@ def _run_both(case, imp_mode):
     sc_ref = scores0.clone()
     sc_new = scores0.clone()
     imp = torch.zeros((H, n_slots), dtype=torch.float32, device=DEV)
+    # the workspace entry point keeps the softmax probabilities for one pass as the
+    # scratch of the allocation-free one does for these sizes
+    ws = torch.empty(max(ops.attention_workspace_floats(plan, H), 4), dtype=torch.float32, device=DEV)
     n_idx = max(int(plan.row_idx.size), 1)
     for first, count, tile_rows in _classes(plan):
         if count == 0:
@@ -68,7 +71,7 @@ def _run_both(case, imp_mode):
                   plan.page_log2, plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(),
                   n_idx, tile_rows, scale)
         lib.call("fdl_block_attention", q.data_ptr(), *common, out_ref.data_ptr(), imp_mode,
-                 imp.data_ptr() if imp_mode else None, stream)
+                 imp.data_ptr() if imp_mode else None, ws.data_ptr(), ws.numel(), stream)
         if imp_mode:
             lib.call("fdl_importance_accumulate", imp.data_ptr(), H, n_slots,
                      plan.page_table_d.data_ptr(), plan.page_table.shape[0],
