@@ -7,6 +7,8 @@
 // For row r with maximum m (first index i_max):
 //   s = sum_j exp(x_j - m) in float64; max probability = exp(0) / s = 1 / s;
 //   probability of token t = exp(x_t - m) / s.
+// A row with a NaN, a +inf or only -inf logits has a softmax of NaNs: probability NaN and
+// index 0, as torch.max returns for it.
 // bf16 -> float -> double is exact, so every term is the float64 softmax term; only the
 // order of the float64 sum differs from torch's reduction.
 #include <stdint.h>
@@ -43,7 +45,8 @@ __global__ __launch_bounds__(kConfThreads) void softmax_conf_kernel(
   const uint16_t* x = logits + int64_t(blockIdx.x) * vocab;
   const int64_t n8 = vocab / 8;
 
-  // pass 1: maximum and its first index (each thread visits increasing indices)
+  // pass 1: maximum and its first index (each thread visits increasing indices; a thread
+  // that visits none keeps the index past every real one)
   float m = -INFINITY;
   int64_t im = INT64_MAX;
   for (int64_t c = tid; c < n8; c += kConfThreads) {
@@ -104,7 +107,9 @@ __global__ __launch_bounds__(kConfThreads) void softmax_conf_kernel(
       p = 1.0 / sum;
     }
     prob[blockIdx.x] = p;
-    if (arg) arg[blockIdx.x] = im;
+    // A row with a NaN (no comparison above selects it, but it makes the sum NaN), a +inf or
+    // only -inf logits has a softmax of NaNs; torch.max of it returns index 0.
+    if (arg) arg[blockIdx.x] = __builtin_isfinite(m) && sum == sum ? im : 0;
   }
 }
 

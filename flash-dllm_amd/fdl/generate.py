@@ -426,6 +426,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             enqueue_rank()
         x0_p_all = x0_p_all.cpu().numpy()
         x0_all = x0_all.cpu().numpy()
+        if len(x0_all) and (x0_all.min() < 0 or x0_all.max() >= logits.shape[-1]):
+            raise RuntimeError(f"token ids outside [0, {logits.shape[-1]}) from the LM head")
         del logits
 
         keep_num = [0] * B

@@ -29,6 +29,13 @@ positions = [query_pos_flat, key_pos_flat, [sin, cos], info, attn_scores, attn_m
 lengths   = [start_layer, query_verify_blocks, query_masked_blocks, query_tracked_blocks,
              query_blocks, active_batch, num_active, max_length, block_m, block_n,
              elastic_cache, verify]
+Where the results differ from the reference's (same arithmetic, different roundings):
+  * x = og_x + ff_out(x) is rounded to bf16 once (the residual rides in the product, or in
+    the split-K reduction), where the reference rounds ff_out(x) and then the sum: the block
+    output can differ in the last bf16 bit;
+  * the verify attention's softmax is exact over both key sets (the reference adds the
+    in-block terms without raising its running maximum, flash_cache_triton.py:416).
+
 `info` (unused by the reference kernels) may carry a precomputed fdl.schedule.AttnPlan;
 otherwise the plan is derived from the masked/tracked block tables once per forward
 (the same table objects are passed to every layer) and reused by all layers. A plan over a

@@ -4,6 +4,7 @@ softmax probability of a given token. The reference is torch's float64 softmax o
 the float64 terms are identical and only the order of the sum differs, so probabilities
 agree to ~1e-13 relative and indices exactly. (torch's float64 softmax kernel on this ROCm
 build is itself ~1e-9 off the CPU result, so it is not the reference here.)"""
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -42,3 +43,21 @@ def test_softmax_confidence_token_probability():
     prob, _ = ops.softmax_confidence(logits.to(DEV), tok.to(DEV))
     torch.cuda.synchronize()
     torch.testing.assert_close(prob.cpu(), ref, rtol=1e-12, atol=1e-300)
+
+
+def test_softmax_confidence_non_finite_rows_match_torch():
+    """Rows of all -inf, with a NaN, with a +inf, and with the maximum tied at several
+    places: the probability and index are torch.max(softmax(float64)) of the row (NaN and
+    index 0 for the rows whose softmax is NaN; the first index of a tie)."""
+    vocab = 1024
+    x = torch.randn((5, vocab), generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    x[0] = float("-inf")
+    x[1, 300] = float("nan")
+    x[2, 700] = float("inf")
+    x[3, 10] = x[3, 500] = x[3, 900] = 8.0  # tied maximum
+    prob, arg = ops.softmax_confidence(x.to(DEV))
+    ref_p, ref_i = torch.max(torch.softmax(x.double(), dim=-1), dim=-1)
+    got_p, got_i = prob.cpu(), arg.cpu()
+    assert torch.equal(got_i, ref_i), (got_i, ref_i)
+    assert torch.isnan(got_p[:3]).all() and torch.isnan(ref_p[:3]).all()
+    np.testing.assert_allclose(got_p[3:].numpy(), ref_p[3:].numpy(), rtol=1e-12)
