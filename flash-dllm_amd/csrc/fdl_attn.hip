@@ -67,7 +67,8 @@ struct AttnArgs {
   const int32_t* row_idx;
   const int64_t* key_slots;  // verify
   const int32_t* vblocks;    // verify
-  const uint8_t* mask;       // verify
+  const uint8_t* mask;       // verify: dense mask, or
+  const int32_t* vmeta;      // verify: (T, S) per block, the closed-form mask
   float* imp_part;
   float* ws;         // softmax importance: probabilities of the importance rows (see kWsBlock)
   int ws_blocks;     // key blocks of room per (work item, head) in ws; 0: no workspace
@@ -354,6 +355,19 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
 constexpr int kStoreRows = 32;
 constexpr int kWsBlock = kStoreRows * kTileN + kStoreRows;
 
+// The Flash-Verify mask of a block of T fill rows, S draft rows and S mask rows (rows and
+// columns in that order; generate.py:260-269): fill rows do not see the drafts; draft i sees
+// drafts j <= i and masks j > i; mask i sees drafts j < i and masks j >= i; everything else
+// is visible.
+__device__ __forceinline__ bool verify_visible(int T, int S, int r, int j) {
+  if (r < T) return j < T || j >= T + S;
+  if (j < T) return true;
+  const bool rd = r < T + S, cd = j < T + S;
+  const int i = rd ? r - T : r - T - S, jj = cd ? j - T : j - T - S;
+  if (rd) return cd ? i >= jj : i < jj;
+  return cd ? i > jj : i <= jj;
+}
+
 // Steps of a tile, the same sequence for producers and consumers (one barrier each):
 //   [0, n_blk)          cache blocks, K and V
 //   [n_blk, 2 n_blk)    softmax importance without the LDS store: the cache blocks again,
@@ -387,16 +401,24 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const int col0 = h * kHeadDim;
 
   int b = 0, k_begin, k_end, n_rows, n_imp = 0, row0 = 0, roff = 0;
+  // verify: block vb_idx, rows [blk_row0 + 128 half, ...) of its n_in rows (all n_in rows
+  // are also its in-block keys)
+  int vb_idx = 0, half_v = 0, blk_row0 = 0, n_in = 0;
   if constexpr (kVerify) {
-    const int32_t* vb = a.vblocks + 4 * blockIdx.x;
+    vb_idx = a.split ? int(blockIdx.x >> 1) : int(blockIdx.x);
+    half_v = a.split ? int(blockIdx.x & 1) : 0;
+    const int32_t* vb = a.vblocks + 4 * vb_idx;
     k_begin = vb[0];
     k_end = vb[1];
-    row0 = vb[2];
-    n_rows = vb[3] - vb[2];
+    blk_row0 = vb[2];
+    n_in = vb[3] - vb[2];
     // out-of-range entries (rejected by the host validator) degrade to an empty range
     if (k_begin < 0 || k_end > a.n_keys) k_end = k_begin;
-    if (row0 < 0 || int64_t(row0) + n_rows > a.n_q_rows) n_rows = 0;
-    if (n_rows > a.block_rows) n_rows = a.block_rows;  // mask rows hold block_rows columns
+    if (blk_row0 < 0 || n_in < 0 || int64_t(blk_row0) + n_in > a.n_q_rows) n_in = 0;
+    if (n_in > a.block_rows) n_in = a.block_rows;  // mask rows hold block_rows columns
+    row0 = blk_row0 + kRows * half_v;
+    n_rows = n_in - kRows * half_v;
+    if (a.split && n_rows <= 0) return;  // an empty upper half
   } else {
     const int half = a.split ? int(blockIdx.x & 1) : 0;
     const int32_t* it = a.work + 8 * (a.split ? blockIdx.x >> 1 : blockIdx.x);
@@ -423,6 +445,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
   const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
   const bool inblock = kVerify && n_rows > 0;
+  const int n_ib = inblock ? (n_in + kTileN - 1) / kTileN : 0;  // in-block key steps
   // softmax importance from the workspace (one pass) or from a second pass over K
   // (64-row tiles only: the 128-row variant's twelve wavefronts leave too few registers)
   const bool store = NC == 4 && imp_soft && n_imp <= kStoreRows && n_blk <= a.ws_blocks;
@@ -430,7 +453,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   float* ws_tile = store ? a.ws + (int64_t(a.split ? blockIdx.x >> 1 : blockIdx.x) * gridDim.y +
                                    blockIdx.y) * a.ws_blocks * kWsBlock
                          : nullptr;
-  const int n_steps = n_blk * (two_pass ? 2 : 1) + (inblock ? 1 : 0);
+  const int n_steps = n_blk * (two_pass ? 2 : 1) + n_ib;
   // Step -> key block: the first pass walks the blocks forward, the second (softmax
   // importance, K only) walks them backward, so it starts with the last kSt blocks of the
   // first pass, which are still in LDS, and continues with the most recently read ones.
@@ -485,7 +508,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     auto issue = [&](int s) {
       if (loads(s) == 0) return;
       uint8_t* st = smem + stage_of(s) * kStageBytes;
-      const bool in_blk = kVerify && inblock && s == n_steps - 1;
+      const bool in_blk = kVerify && s >= n_blk;
       const bool k_only = !kVerify && s >= n_blk;
       const int n0 = k_begin + kTileN * block_of(s);
 #pragma unroll
@@ -494,7 +517,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         const int key = 4 * q + (lane >> 4);
         const uint16_t *ks, *vs;
         if (in_blk) {
-          const int64_t r = int64_t(row0) + min(key, n_rows - 1);  // rows checked above
+          // in-block key 64 (s - n_blk) + key: query row blk_row0 + that (checked above)
+          const int64_t r = int64_t(blk_row0) + min(kTileN * (s - n_blk) + key, n_in - 1);
           ks = a.kblk + r * D + col0;
           vs = a.vblk + r * D + col0;
         } else {
@@ -627,17 +651,25 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
     const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
     const bool pass2 = !kVerify && s >= n_blk;
-    const bool in_blk = kVerify && inblock && s == n_steps - 1;
+    const bool in_blk = kVerify && inblock && s >= n_blk;
     const int n0 = k_begin + kTileN * block_of(s);
     if (two_pass && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
     if (in_blk) {
       const int br = a.block_rows;
+      const int j0 = kTileN * (s - n_blk);  // first in-block key of the step
+      int vT = 0, vS = 0;
+      if (a.vmeta) {
+        vT = a.vmeta[2 * vb_idx];
+        vS = a.vmeta[2 * vb_idx + 1];
+      }
       attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
-        const int r = 16 * (wr * RB + rb) + l16;
-        const int j = 16 * kb + 4 * g + ii;
-        return j < n_rows && r < br && a.mask[(int64_t(blockIdx.x) * br + r) * br + j] != 0
-                   ? 0.f
-                   : -INFINITY;
+        const int r = 16 * (wr * RB + rb) + l16;  // row of this workgroup
+        const int rr = r + kRows * half_v;          // row of the block
+        const int j = j0 + 16 * kb + 4 * g + ii;
+        if (j >= n_in || r >= n_rows) return -INFINITY;
+        const bool vis = a.vmeta ? verify_visible(vT, vS, rr, j)
+                                 : a.mask[(int64_t(vb_idx) * br + rr) * br + j] != 0;
+        return vis ? 0.f : -INFINITY;
       }, [](int, const f32x4 (&)[4], float) {});
     } else if (!pass2) {
       // keys past k_end (the tail of the last block) get a -infinity bias
@@ -1495,8 +1527,9 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
                                     int64_t n_slots, int64_t d_model, int64_t n_heads,
                                     int64_t head_dim, const int64_t* key_slots, int64_t n_keys,
                                     const int32_t* vblocks, int64_t n_vblocks,
-                                    const uint8_t* mask, int32_t block_rows,
-                                    float softmax_scale, void* out, void* stream) {
+                                    const uint8_t* mask, const int32_t* vmeta,
+                                    int32_t block_rows, float softmax_scale, void* out,
+                                    void* stream) {
   using namespace fdl;
   FDL_REQUIRE(n_vblocks >= 0 && n_vblocks < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_verify_attention: n_vblocks = %lld out of range", (long long)n_vblocks);
@@ -1507,11 +1540,12 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   FDL_REQUIRE_PTR(k_blk);
   FDL_REQUIRE_PTR(v_blk);
   FDL_REQUIRE_PTR(vblocks);
-  FDL_REQUIRE_PTR(mask);
+  FDL_REQUIRE((mask != nullptr) != (vmeta != nullptr), FDL_ERR_NULL,
+              "fdl_verify_attention: exactly one of mask and vmeta must be given");
   FDL_REQUIRE((reinterpret_cast<uintptr_t>(k_blk) | reinterpret_cast<uintptr_t>(v_blk)) % 16 == 0,
               FDL_ERR_SHAPE, "fdl_verify_attention: k_blk/v_blk must be 16-byte aligned");
-  FDL_REQUIRE(block_rows >= 1 && block_rows <= 64, FDL_ERR_UNSUPPORTED,
-              "fdl_verify_attention: block_rows = %d outside [1, 64]", block_rows);
+  FDL_REQUIRE(block_rows >= 1 && block_rows <= 256, FDL_ERR_UNSUPPORTED,
+              "fdl_verify_attention: block_rows = %d outside [1, 256]", block_rows);
   FDL_REQUIRE(n_keys >= 0 && n_keys < (int64_t(1) << 31), FDL_ERR_SHAPE,
               "fdl_verify_attention: n_keys out of range");
   FDL_REQUIRE(n_keys == 0 || key_slots != nullptr, FDL_ERR_NULL,
@@ -1527,6 +1561,7 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   args.key_slots = key_slots;
   args.vblocks = vblocks;
   args.mask = mask;
+  args.vmeta = vmeta;
   args.block_rows = block_rows;
   args.n_slots = n_slots;
   args.n_q_rows = n_q_rows;
@@ -1534,7 +1569,17 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   args.d_model = static_cast<int>(d_model);
   args.scale_log2 = softmax_scale * kLog2e;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = launch_attn<1, 4, true>(args, n_vblocks, n_heads, s);
+  // up to 64 rows per block: 64-row tiles; up to 128: 128-row tiles; up to 256: two 128-row
+  // workgroups per block (each attends to every in-block key)
+  hipError_t e;
+  if (block_rows <= 64) {
+    e = launch_attn<1, 4, true>(args, n_vblocks, n_heads, s);
+  } else {
+    FDL_REQUIRE(n_vblocks < (int64_t(1) << 30), FDL_ERR_SHAPE,
+                "fdl_verify_attention: n_vblocks out of range");
+    args.split = block_rows > 128 ? 1 : 0;
+    e = launch_attn<1, 8, true>(args, block_rows > 128 ? 2 * n_vblocks : n_vblocks, n_heads, s);
+  }
   FDL_HIP_CHECK(e);
   return ok();
 }

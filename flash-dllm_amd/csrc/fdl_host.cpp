@@ -118,8 +118,8 @@ extern "C" int fdl_validate_vblocks(const int32_t* vblocks, int64_t n_vblocks,
                                     const int64_t* key_slots, int64_t n_keys, int64_t n_q_rows,
                                     int64_t n_slots, int32_t block_rows) {
   FDL_REQUIRE(n_vblocks >= 0, FDL_ERR_SHAPE, "fdl_validate_vblocks: n_vblocks < 0");
-  FDL_REQUIRE(block_rows >= 1 && block_rows <= 64, FDL_ERR_SHAPE,
-              "fdl_validate_vblocks: block_rows = %d outside [1, 64]", block_rows);
+  FDL_REQUIRE(block_rows >= 1 && block_rows <= 256, FDL_ERR_SHAPE,
+              "fdl_validate_vblocks: block_rows = %d outside [1, 256]", block_rows);
   if (n_vblocks == 0) return fdl::ok();
   FDL_REQUIRE_PTR(vblocks);
   for (int64_t v = 0; v < n_vblocks; ++v) {

@@ -105,7 +105,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _p, _p, _p, _p,           # q, k_blk, v_blk, k_cache, v_cache
         _i64, _i64, _i64, _i64, _i64,  # n_q_rows, n_slots, d_model, n_heads, head_dim
         _p, _i64, _p, _i64,           # key_slots, n_keys, vblocks, n_vblocks
-        _p, _i32, _f32, _p, _p,       # mask, block_rows, softmax_scale, out, stream
+        _p, _p, _i32, _f32, _p, _p,   # mask, vmeta, block_rows, softmax_scale, out, stream
     ]),
     "fdl_rms_norm": (ctypes.c_int, [
         _p, _p, _p,                   # x, residual, weight

@@ -219,7 +219,9 @@ def verify_attention(q: torch.Tensor, k_blk: torch.Tensor, v_blk: torch.Tensor,
                      k_cache: torch.Tensor, v_cache: torch.Tensor, key_slots: torch.Tensor,
                      vblocks: torch.Tensor, mask: torch.Tensor, block_rows: int,
                      out: torch.Tensor, n_heads: int, softmax_scale: float) -> None:
-    """Flash-Verify attention (fdl_verify_attention)."""
+    """Flash-Verify attention (fdl_verify_attention). `mask` is the reference's boolean
+    [n_blocks * block_rows, block_rows] mask, or int32 [n_blocks, 2] = (T, S) per block for
+    the closed-form mask (no mask read from memory)."""
     dev = q.device
     _need(q, "q", BF16, 2)
     for n, t in (("k_blk", k_blk), ("v_blk", v_blk), ("out", out)):
@@ -230,18 +232,25 @@ def verify_attention(q: torch.Tensor, k_blk: torch.Tensor, v_blk: torch.Tensor,
     _need(v_cache, "v_cache", BF16, 2, dev)
     _need(key_slots, "key_slots", torch.int64, 1, dev)
     _need(vblocks, "vblocks", torch.int32, 2, dev)
-    if mask.dtype == torch.bool:
-        mask = mask.view(torch.uint8)
-    _need(mask, "mask", torch.uint8, 2, dev)
     nv = vblocks.shape[0]
-    if tuple(mask.shape) != (nv * block_rows, block_rows):
-        raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"mask must be [{nv * block_rows}, {block_rows}]")
+    vmeta = None
+    if mask.dtype == torch.int32:
+        vmeta, mask = mask, None
+        _need(vmeta, "vmeta", torch.int32, 2, dev)
+        if tuple(vmeta.shape) != (nv, 2):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"vmeta must be [{nv}, 2]")
+    else:
+        if mask.dtype == torch.bool:
+            mask = mask.view(torch.uint8)
+        _need(mask, "mask", torch.uint8, 2, dev)
+        if tuple(mask.shape) != (nv * block_rows, block_rows):
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"mask must be [{nv * block_rows}, {block_rows}]")
     d_model = q.shape[1]
     _lib.call("fdl_verify_attention", q.data_ptr(), k_blk.data_ptr(), v_blk.data_ptr(),
               k_cache.data_ptr(), v_cache.data_ptr(), q.shape[0], k_cache.shape[0], d_model,
               n_heads, d_model // n_heads, key_slots.data_ptr() if key_slots.numel() else None,
-              key_slots.numel(), vblocks.data_ptr(), nv, mask.data_ptr(), int(block_rows),
-              float(softmax_scale), out.data_ptr(), _stream(q))
+              key_slots.numel(), vblocks.data_ptr(), nv, _ptr(mask), _ptr(vmeta),
+              int(block_rows), float(softmax_scale), out.data_ptr(), _stream(q))
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,

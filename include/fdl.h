@@ -212,10 +212,16 @@ int fdl_importance_accumulate_rank(const float* imp_part, int64_t n_heads, float
  * as in-block keys (k_blk/v_blk, packed by row) under the block's boolean mask.
  *   q, k_blk, v_blk bf16 [n_q_rows][d_model]    (outputs of fdl_qkv_rope_cache, kv_packed=1)
  *   key_slots int64 [n_keys]
- *   vblocks  int32 [n_vblocks][4]; q1 - q0 <= block_rows <= 64
+ *   vblocks  int32 [n_vblocks][4]; q1 - q0 <= block_rows <= 256 (the reference's 2 * block_m)
+ *   exactly one of
  *   mask     uint8 [n_vblocks * block_rows][block_rows]; row i of block v is
- *            mask[v*block_rows + i]; nonzero = may attend. Column j is additionally
- *            valid only if q0 + j < q1.
+ *            mask[v*block_rows + i]; nonzero = may attend (the reference's attn_mask), or
+ *   vmeta    int32 [n_vblocks][2] = (T, S): the block's rows are T fill rows, S draft rows
+ *            and S mask rows (T + 2S = q1 - q0), and the mask is the reference's closed form
+ *            (generate.py:260-269): fill rows do not see the drafts, draft i sees drafts
+ *            j <= i and masks j > i, mask i sees drafts j < i and masks j >= i, all else is
+ *            visible. No mask is read from memory.
+ *   Column j is additionally valid only if q0 + j < q1.
  *   out      bf16 [n_q_rows][d_model]
  * Softmax is exact over the union of both key sets (the running maximum includes the
  * in-block logits).
@@ -224,8 +230,8 @@ int fdl_verify_attention(const void* q, const void* k_blk, const void* v_blk,
                          const void* k_cache, const void* v_cache, int64_t n_q_rows,
                          int64_t n_slots, int64_t d_model, int64_t n_heads, int64_t head_dim,
                          const int64_t* key_slots, int64_t n_keys, const int32_t* vblocks,
-                         int64_t n_vblocks, const uint8_t* mask, int32_t block_rows,
-                         float softmax_scale, void* out, void* stream);
+                         int64_t n_vblocks, const uint8_t* mask, const int32_t* vmeta,
+                         int32_t block_rows, float softmax_scale, void* out, void* stream);
 
 /*
  * Host-side validators (host pointers; no GPU needed). They return FDL_ERR_RANGE with a

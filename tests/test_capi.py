@@ -67,7 +67,7 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_SHAPE, "fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 17,
             None, None, 10, None, 10, None, 1, 16, None, 0, None)
     _expect(lib.FDL_ERR_NULL, "fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32,
-            128, None, 0, None, 1, None, 64, 0.1, None, None)
+            128, None, 0, None, 1, None, None, 64, 0.1, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 1,
             1.0, None, None)
     assert lib.load().fdl_last_error().decode().startswith("fdl_importance_accumulate")
@@ -89,7 +89,7 @@ def test_launchers_reject_bad_scalars_without_gpu():
              None, 10, None, 0, 16, None, 0, None)
     lib.call("fdl_importance_accumulate", None, 32, 10, None, 1, 1, 5, None, 0, 1.0, None, None)
     lib.call("fdl_verify_attention", None, None, None, None, None, 4, 4, 4096, 32, 128, None, 0,
-             None, 0, None, 64, 0.1, None, None)
+             None, 0, None, None, 64, 0.1, None, None)
     lib.call("fdl_rms_norm", None, None, None, 0, 4096, 1e-5, None, None, None)
     lib.call("fdl_silu_mul", None, None, 0, None, None)
 
@@ -181,4 +181,5 @@ def test_validate_vblocks():
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 10, 8)   # slot 10
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 4, 16, 11, 8)   # k1 > n_keys
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 7)   # 8 rows > 7
-    _expect(lib.FDL_ERR_SHAPE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 65)
+    lib.call("fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 256)   # 2 * block_m up to 256
+    _expect(lib.FDL_ERR_SHAPE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 257)

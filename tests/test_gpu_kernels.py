@@ -525,17 +525,19 @@ def test_importance_accumulate_rank_matches_separate_kernels(L, H):
 
 # -------------------------------------------------------------------------- verify
 
-def _verify_case(seed, n_blk, k_cache_len, H, bm=32):
+def _verify_case(seed, n_blk, k_cache_len, H, bm=32, with_ts=False, s_min=4):
     """Verify blocks in the reference layout (llada/generate.py:260-292): T fill rows,
-    S draft rows, S mask rows; keys are all cache slots except fill and candidates."""
+    S draft rows, S mask rows; keys are all cache slots except fill and candidates. With
+    with_ts, also returns the (T, S) of every block."""
     rng = np.random.default_rng(seed)
     rows = 2 * bm
     L = k_cache_len
-    key_pos, vblocks, masks, qslots = [], [], [], []
+    key_pos, vblocks, masks, qslots, ts = [], [], [], [], []
     acc_k = 0
     for j in range(n_blk):
-        S = int(rng.integers(4, bm // 2 + 1))
+        S = int(rng.integers(s_min, bm // 2 + 1))
         T = rows - 2 * S
+        ts.append((T, S))
         nd = int(rng.integers(T + 64, L - S - 1))
         order = np.arange(L)
         fill = order[nd - T:nd]
@@ -546,8 +548,72 @@ def _verify_case(seed, n_blk, k_cache_len, H, bm=32):
         acc_k += len(keys)
         masks.append(orc.verify_mask(T, S, bm))
         qslots.append(np.concatenate([fill, cand, cand]) + j * L)
-    return (np.concatenate(key_pos).astype(np.int64), np.asarray(vblocks, np.int32),
-            np.concatenate(masks), np.concatenate(qslots).astype(np.int64))
+    out = (np.concatenate(key_pos).astype(np.int64), np.asarray(vblocks, np.int32),
+           np.concatenate(masks), np.concatenate(qslots).astype(np.int64))
+    return out + (np.asarray(ts, np.int32),) if with_ts else out
+
+
+@pytest.mark.parametrize("bm", [32, 64, 128])
+def test_verify_attention_block_rows_up_to_256_and_closed_form_mask(bm):
+    """Verify blocks of 2 block_m = 64, 128 and 256 rows (the reference's block_length 32,
+    64 and the default 128): 64-row tiles, 128-row tiles, and two 128-row workgroups per
+    block, each attending to every in-block key (1, 2 or 4 in-block key blocks). The
+    attention with the reference's dense mask matches the oracle, and the closed-form mask
+    from each block's (T, S) gives the same output bit for bit."""
+    H, n_blk, L = 8, 6, 1024
+    key_pos, vblocks, mask, _, ts = _verify_case(21 + bm, n_blk, L, H, bm, with_ts=True, s_min=1)
+    rows = 2 * bm
+    gen = torch.Generator().manual_seed(22)
+    D = H * 128
+    q, k1, v1 = (_bf16((n_blk * rows, D), gen) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen) for _ in range(2))
+    args = [t.to(DEV) for t in (q, k1, v1, kc, vc)] + [torch.from_numpy(key_pos).to(DEV),
+                                                       torch.from_numpy(vblocks).to(DEV)]
+    scale = orc.softmax_scale(128)
+    out_dense = torch.full((n_blk * rows, D), POISON, dtype=torch.bfloat16, device=DEV)
+    out_ts = torch.full_like(out_dense, POISON)
+    ops.verify_attention(*args, torch.from_numpy(mask).to(DEV), rows, out_dense, H, scale)
+    ops.verify_attention(*args, torch.from_numpy(ts).to(DEV), rows, out_ts, H, scale)
+    torch.cuda.synchronize()
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, rows, H, scale)
+    _close(_np(out_dense), ref, what=f"verify attention, {rows}-row blocks")
+    assert torch.equal(out_ts, out_dense)
+
+
+def test_verify_attention_closed_form_without_fill_rows():
+    """T = 0 (2S rows of drafts then masks, the verify-query workload's layout): the
+    closed-form mask against the oracle's mask construction."""
+    H, n_blk, L, bm = 4, 5, 512, 16
+    rng = np.random.default_rng(31)
+    key_pos, vblocks, masks, ts = [], [], [], []
+    acc_k = acc_q = 0
+    for j in range(n_blk):
+        S = int(rng.integers(1, bm + 1))
+        cand = j * L + 200 + np.arange(S)
+        keys = np.setdiff1d(j * L + np.arange(L), cand)
+        key_pos.append(keys)
+        vblocks.append((acc_k, acc_k + len(keys), acc_q, acc_q + 2 * S))
+        acc_k += len(keys)
+        acc_q += 2 * S
+        masks.append(orc.verify_mask(0, S, bm))
+        ts.append((0, S))
+    key_pos = np.concatenate(key_pos).astype(np.int64)
+    vblocks = np.asarray(vblocks, np.int32)
+    mask = np.concatenate(masks)
+    gen = torch.Generator().manual_seed(32)
+    D = H * 128
+    q, k1, v1 = (_bf16((acc_q, D), gen) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen) for _ in range(2))
+    out = torch.full((acc_q, D), POISON, dtype=torch.bfloat16, device=DEV)
+    ops.verify_attention(*(t.to(DEV) for t in (q, k1, v1, kc, vc)), torch.from_numpy(key_pos).to(DEV),
+                         torch.from_numpy(vblocks).to(DEV),
+                         torch.from_numpy(np.asarray(ts, np.int32)).to(DEV), 2 * bm, out, H,
+                         orc.softmax_scale(128))
+    torch.cuda.synchronize()
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, 2 * bm, H, orc.softmax_scale(128))
+    _close(_np(out), ref, what="verify attention, closed-form mask, no fill rows")
 
 
 def test_verify_attention_batch16_cache1024():
