@@ -24,7 +24,8 @@ LIB_PATH = PKG_DIR / "libfdl.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
-HIP_SOURCES = ["fdl_qkv.hip", "fdl_attn.hip", "fdl_rank.hip", "fdl_block.hip", "fdl_head.hip"]
+HIP_SOURCES = ["fdl_qkv.hip", "fdl_attn.hip", "fdl_rank.hip", "fdl_block.hip", "fdl_head.hip",
+               "fdl_sched.hip"]
 CXX_SOURCES = ["fdl_host.cpp"]
 
 HIPCC_FLAGS = [

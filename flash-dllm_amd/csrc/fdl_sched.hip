@@ -1,0 +1,477 @@
+// Device-side decode scheduler of the Flash-Cache + Flash-Verify loop (gfx950).
+//
+// The bookkeeping of llada/generate.py:125-470 kept in device memory, so that a denoising
+// step runs its pass-1 forward, the verify forward and the ranking back to back and the host
+// synchronises once per step (to learn the next step's row counts and completions):
+//   sched_pass1_kernel   pass-1 acceptance (generate.py:215-258 with Flash-Verify,
+//                        :335-350 without) and the Flash-Verify lists: fill rows, candidate
+//                        draft and mask rows, the key list and the per-block (T, S) of the
+//                        closed-form mask (:260-297)
+//   sched_verify_kernel  verify acceptance: cumulative product of the mask rows' draft-token
+//                        probabilities against gamma (:307-333)
+//   sched_pack_kernel    completion test and the next step's masked / tracked lists
+//                        (:364-383), packed as the reference packs them (:439-467): masked
+//                        rows of every sequence, then tracked rows; plus the attention work
+//                        items of that packing
+// The ranking itself (:364-366) is fdl_importance_rank / fdl_importance_accumulate_rank on
+// the segments the acceptance kernels write.
+//
+// All three run as one workgroup (the per-step work is a few thousand integers): a wavefront
+// per sequence where rows are involved, thread 0 for the prefix sums across sequences.
+#include <stdint.h>
+
+#include "fdl_device.h"
+#include "fdl_host.h"
+
+namespace fdl {
+namespace {
+
+constexpr int kSchedThreads = 256;
+constexpr int kSchedWaves = kSchedThreads / kWave;
+constexpr int kMaxBm = 128;   // block_m
+constexpr int kMaxSeq = 256;  // sequences (batch rows)
+
+struct SchedArgs {
+  fdl_sched s;
+};
+
+__device__ __forceinline__ int32_t* seq_of(const fdl_sched& s, int j) {
+  return s.seq + FDL_SCHED_SEQ_FIELDS * j;
+}
+
+// Row i of the pass-1 confidences ranks before row k in the stable descending sort
+// (generate.py:230, :343; numpy's argsort of -conf, kind="stable", puts NaN last).
+__device__ __forceinline__ bool conf_before(double ck, int k, double ci, int i) {
+  const bool nk = ck != ck, ni = ci != ci;
+  if (nk != ni) return ni;                 // a number before a NaN
+  if (nk || ck == ci) return k < i;        // equal (or both NaN): lower row first
+  return ck > ci;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ int64_t wave_max(int64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int64_t o = __shfl_xor(v, off);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v |= __shfl_xor(v, off);
+  return v;
+}
+
+// ------------------------------------------------------------------------------- pass 1
+__global__ __launch_bounds__(kSchedThreads) void sched_pass1_kernel(
+    fdl_sched s, const double* __restrict__ conf, const int64_t* __restrict__ tok) {
+  __shared__ int s_off[kMaxSeq];   // first pass-1 row of sequence j (-1: inactive)
+  __shared__ int s_act[kMaxSeq];   // index among the active sequences
+  __shared__ int64_t s_koff[kMaxSeq];
+  __shared__ double s_c[kSchedWaves][kMaxBm];
+  __shared__ int64_t s_p[kSchedWaves][kMaxBm];
+  __shared__ int64_t s_t[kSchedWaves][kMaxBm];
+  __shared__ int s_dec[kSchedWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = static_cast<int>(s.n_seq);
+  const int64_t L = s.max_length;
+  const int bm = s.block_m;
+  if (tid == 0) {
+    int acc = 0, na = 0;
+    for (int j = 0; j < B; ++j) {
+      const int32_t* q = seq_of(s, j);
+      if (q[FDL_SEQ_ACTIVE] < 0) {
+        s_off[j] = -1;
+        s_act[j] = -1;
+        continue;
+      }
+      s_off[j] = acc;
+      s_act[j] = na++;
+      acc += q[FDL_SEQ_N_MASKED];
+    }
+  }
+  if (lane == 0) s_dec[wave] = 0;
+  __syncthreads();
+  for (int j = wave; j < B; j += kSchedWaves) {
+    if (s_off[j] < 0) continue;
+    int32_t* q = seq_of(s, j);
+    const int nm = q[FDL_SEQ_N_MASKED], nd0 = q[FDL_SEQ_ND];
+    const int64_t eos = q[FDL_SEQ_EOS], pred = q[FDL_SEQ_PRED];
+    int64_t* fp = s.full_pos + j * L;
+    int n_lmask = 0, n_hi = 0;
+    for (int i = lane; i < nm; i += kWave) {
+      double c = conf[s_off[j] + i];
+      const int64_t p = fp[nd0 + i];
+      if (eos != -1 && p >= pred) {  // the predicted-length mask (generate.py:219-225, :339)
+        c = 0.0;
+        ++n_lmask;
+      }
+      n_hi += c >= s.threshold;
+      s_c[wave][i] = c;
+      s_p[wave][i] = p;
+      s_t[wave][i] = tok[s_off[j] + i];
+    }
+    n_lmask = wave_sum(n_lmask);
+    n_hi = wave_sum(n_hi);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int keep = n_hi > 1 ? n_hi : 1;  // at least one token per step
+    int64_t ecand = -1;
+    for (int i = lane; i < nm; i += kWave) {
+      const double ci = s_c[wave][i];
+      int rank = 0;
+      for (int k = 0; k < nm; ++k) rank += conf_before(s_c[wave][k], k, ci, i);
+      const int64_t p = s_p[wave][i], t = s_t[wave][i];
+      fp[nd0 + rank] = p;                    // full_pos[nd : nd + nm] = masked[order]
+      if (s.verify) s.x_draft[p] = t;        // x_draft[masked] = x0
+      if (rank < keep) {
+        s.x[p] = t;
+        if (t == s.eos_id) ecand = p > ecand ? p : ecand;
+      }
+    }
+    ecand = wave_max(ecand);
+    if (lane == 0) {
+      const int nd = nd0 + keep;
+      q[FDL_SEQ_ND] = nd;
+      if (eos == -1 && ecand >= 0) {
+        q[FDL_SEQ_EOS] = static_cast<int32_t>(ecand);
+        q[FDL_SEQ_PRED] = static_cast<int32_t>(ecand + 1);
+      }
+      q[FDL_SEQ_KEEP] = keep;
+      s_dec[wave] += keep;
+      if (!s.verify) {
+        s.seg[2 * s_act[j]] = static_cast<int32_t>(j * L);
+        s.seg[2 * s_act[j] + 1] = nd - keep;
+      } else {
+        const int length_num = nm - n_lmask;
+        int S = length_num - keep;
+        S = S < 0 ? 0 : (S > bm / 2 ? bm / 2 : S);
+        int T = 2 * bm - 2 * S;
+        if (nd < T) {  // fewer decoded slots than fill rows: raised by the host
+          q[FDL_SEQ_ERR] = 1;
+          T = nd;
+          S = 0;
+        }
+        q[FDL_SEQ_T] = T;
+        q[FDL_SEQ_S] = S;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int dec = 0;
+    for (int w = 0; w < kSchedWaves; ++w) dec += s_dec[w];
+    s.summary[FDL_SUM_DECODED] += dec;
+  }
+  if (!s.verify) return;
+  // Flash-Verify lists: block a (the a-th active sequence) holds rows [2 bm a, 2 bm (a + 1)):
+  // T fill rows, S draft rows, S mask rows; its keys are full_pos[:nd - T] and
+  // full_pos[nd + S : seqlen_k] (generate.py:272-297).
+  if (tid == 0) {
+    int64_t koff = 0;
+    for (int j = 0; j < B; ++j) {
+      if (s_act[j] < 0) continue;
+      const int32_t* q = seq_of(s, j);
+      const int nd = q[FDL_SEQ_ND], T = q[FDL_SEQ_T], S = q[FDL_SEQ_S], sk = q[FDL_SEQ_SEQLEN_K];
+      const int64_t nk1 = nd - T, nk2 = sk - nd - S > 0 ? sk - nd - S : 0;
+      const int a = s_act[j];
+      s_koff[j] = koff;
+      s.vblocks[4 * a] = static_cast<int32_t>(koff);
+      s.vblocks[4 * a + 1] = static_cast<int32_t>(koff + nk1 + nk2);
+      s.vblocks[4 * a + 2] = 2 * bm * a;
+      s.vblocks[4 * a + 3] = 2 * bm * (a + 1);
+      s.vmeta[2 * a] = T;
+      s.vmeta[2 * a + 1] = S;
+      koff += nk1 + nk2;
+    }
+  }
+  __syncthreads();
+  for (int j = wave; j < B; j += kSchedWaves) {
+    if (s_act[j] < 0) continue;
+    const int32_t* q = seq_of(s, j);
+    const int nd = q[FDL_SEQ_ND], T = q[FDL_SEQ_T], S = q[FDL_SEQ_S], sk = q[FDL_SEQ_SEQLEN_K];
+    const int a = s_act[j];
+    const int64_t* fp = s.full_pos + j * L;
+    const int64_t r0 = int64_t(2) * bm * a;
+    for (int r = lane; r < 2 * bm; r += kWave) {
+      // rows: fill full_pos[nd - T + r], drafts and masks of candidate full_pos[nd + i]
+      int64_t pos;
+      int64_t t;
+      if (r < T) {
+        pos = fp[nd - T + r];
+        t = s.x[pos];
+      } else if (r < T + S) {
+        pos = fp[nd + r - T];
+        t = s.x_draft[pos];
+      } else if (r < T + 2 * S) {
+        pos = fp[nd + r - T - S];
+        t = s.x[pos];
+      } else {  // only after a fill-row shortfall (the host raises)
+        pos = fp[0];
+        t = s.x[pos];
+      }
+      s.vpos[r0 + r] = pos;
+      s.xv[r0 + r] = t;
+    }
+    const int64_t nk1 = nd - T, nk2 = sk - nd - S > 0 ? sk - nd - S : 0;
+    int64_t* kp = s.key_pos + s_koff[j];
+    for (int64_t i = lane; i < nk1 + nk2; i += kWave) kp[i] = i < nk1 ? fp[i] : fp[nd + S + (i - nk1)];
+    // draft tokens of the last bm / 2 rows of the block (the LM head rows of the verify
+    // pass): its mask rows are the last S of them; the others get no token
+    const int tail = bm / 2;
+    for (int r = lane; r < tail; r += kWave) {
+      const int i = r - (tail - S);
+      s.draft_tok[int64_t(tail) * a + r] = i >= 0 ? s.x_draft[fp[nd + i]] : -1;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------ verify accept
+__global__ __launch_bounds__(kSchedThreads) void sched_verify_kernel(fdl_sched s,
+                                                                     const double* __restrict__ prob) {
+  __shared__ int s_act[kMaxSeq];
+  __shared__ int s_dec;
+  const int tid = threadIdx.x;
+  const int B = static_cast<int>(s.n_seq);
+  const int64_t L = s.max_length;
+  const int tail = s.block_m / 2;
+  if (tid == 0) {
+    int na = 0;
+    for (int j = 0; j < B; ++j) s_act[j] = seq_of(s, j)[FDL_SEQ_ACTIVE] < 0 ? -1 : na++;
+    s_dec = 0;
+  }
+  __syncthreads();
+  for (int j = tid; j < B; j += kSchedThreads) {
+    if (s_act[j] < 0) continue;
+    int32_t* q = seq_of(s, j);
+    const int a = s_act[j];
+    const int S = q[FDL_SEQ_S], nd = q[FDL_SEQ_ND];
+    const int64_t eos = q[FDL_SEQ_EOS], pred = q[FDL_SEQ_PRED];
+    const int64_t* fp = s.full_pos + j * L;
+    // cumprod of the mask rows' draft-token probabilities, left to right (generate.py:318-331)
+    double cp = 1.0;
+    int keep = 0;
+    for (int i = 0; i < S; ++i) {
+      double p = prob[int64_t(tail) * a + (tail - S) + i];
+      if (eos != -1 && fp[nd + i] >= pred) p = 0.0;
+      cp *= p;
+      keep += cp >= s.gamma;
+    }
+    int64_t ecand = -1;
+    for (int i = 0; i < keep; ++i) {
+      const int64_t pos = fp[nd + i];
+      const int64_t t = s.x_draft[pos];
+      s.x[pos] = t;
+      if (t == s.eos_id) ecand = pos > ecand ? pos : ecand;
+    }
+    const int ndn = nd + keep;
+    q[FDL_SEQ_ND] = ndn;
+    q[FDL_SEQ_KEEP] = keep;
+    if (eos == -1 && ecand >= 0) {
+      q[FDL_SEQ_EOS] = static_cast<int32_t>(ecand);
+      q[FDL_SEQ_PRED] = static_cast<int32_t>(ecand + 1);
+    }
+    s.seg[2 * a] = static_cast<int32_t>(j * L);
+    s.seg[2 * a + 1] = ndn - keep;
+    atomicAdd(&s_dec, keep);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    s.summary[FDL_SUM_DECODED] += s_dec;
+    s.summary[FDL_SUM_VERIFY_ACCEPTED] += s_dec;
+  }
+}
+
+// --------------------------------------------------------------------------------- pack
+__global__ __launch_bounds__(kSchedThreads) void sched_pack_kernel(fdl_sched s) {
+  __shared__ int s_moff[kMaxSeq], s_toff[kMaxSeq], s_roff[kMaxSeq], s_woff[kMaxSeq];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = static_cast<int>(s.n_seq);
+  const int64_t L = s.max_length;
+  const int bm = s.block_m;
+  // completion (generate.py:384: any undecoded position before the predicted length) and the
+  // next step's lists (:367-381; a newly admitted sequence recomputes every slot, :125-134)
+  for (int j = wave; j < B; j += kSchedWaves) {
+    int32_t* q = seq_of(s, j);
+    if (q[FDL_SEQ_ACTIVE] < 0) continue;
+    const int nd = q[FDL_SEQ_ND], sk = q[FDL_SEQ_SEQLEN_K];
+    const bool fresh = q[FDL_SEQ_FRESH] != 0;
+    const int64_t pred = q[FDL_SEQ_PRED];
+    const int64_t* fp = s.full_pos + j * L;
+    int open = 0;
+    for (int64_t i = nd + lane; i < L && !open; i += kWave) open |= fp[i] < pred;
+    open = wave_or(open);
+    if (lane == 0) {
+      const bool done = !fresh && !open;
+      q[FDL_SEQ_DONE] = done;
+      q[FDL_SEQ_FRESH] = 0;
+      int nm = 0, nt = 0, t0 = 0, t1 = 0;
+      if (!done) {
+        nm = static_cast<int>(L - nd < bm ? L - nd : bm);
+        if (fresh || s.track_num < 0) {
+          t0 = 0;
+          t1 = sk;
+        } else {
+          t0 = nd - s.track_num * bm > 0 ? nd - s.track_num * bm : 0;
+          t1 = nd + bm * s.mask_num < sk ? nd + bm * s.mask_num : sk;
+        }
+        nt = (nd - t0) + (t1 - (nd + bm) > 0 ? t1 - (nd + bm) : 0);
+      }
+      q[FDL_SEQ_N_MASKED] = nm;
+      q[FDL_SEQ_N_TRACKED] = nt;
+      q[FDL_SEQ_T0] = t0;
+      q[FDL_SEQ_T1] = t1;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // packed rows: masked rows of every sequence, then tracked rows (generate.py:439-467);
+    // work items by class (long: more than 128 rows, in 256-row tiles; mid: 65-128; short),
+    // each class in sequence order, row lists in the same order as the items
+    int acc = 0, n_cont = 0, n_done = 0;
+    for (int j = 0; j < B; ++j) {
+      const int32_t* q = seq_of(s, j);
+      s_moff[j] = acc;
+      if (q[FDL_SEQ_ACTIVE] >= 0) {
+        acc += q[FDL_SEQ_N_MASKED];
+        if (q[FDL_SEQ_DONE]) ++n_done;
+        else ++n_cont;
+      }
+    }
+    const int n_masked_rows = acc;
+    for (int j = 0; j < B; ++j) {
+      const int32_t* q = seq_of(s, j);
+      s_toff[j] = acc;
+      if (q[FDL_SEQ_ACTIVE] >= 0) acc += q[FDL_SEQ_N_TRACKED];
+    }
+    int cnt[3] = {0, 0, 0}, rows[3] = {0, 0, 0};
+    for (int j = 0; j < B; ++j) {
+      const int32_t* q = seq_of(s, j);
+      const int n = q[FDL_SEQ_ACTIVE] >= 0 ? q[FDL_SEQ_N_MASKED] + q[FDL_SEQ_N_TRACKED] : 0;
+      if (n == 0) continue;
+      const int cls = n <= 64 ? 2 : (n <= 128 ? 1 : 0);
+      cnt[cls] += cls == 0 ? (n + 255) / 256 : 1;
+      rows[cls] += n;
+    }
+    int wbase[3] = {0, cnt[0], cnt[0] + cnt[1]};
+    int rbase[3] = {0, rows[0], rows[0] + rows[1]};
+    for (int j = 0; j < B; ++j) {
+      const int32_t* q = seq_of(s, j);
+      const int n = q[FDL_SEQ_ACTIVE] >= 0 ? q[FDL_SEQ_N_MASKED] + q[FDL_SEQ_N_TRACKED] : 0;
+      s_roff[j] = -1;
+      if (n == 0) continue;
+      const int cls = n <= 64 ? 2 : (n <= 128 ? 1 : 0);
+      s_roff[j] = rbase[cls];
+      s_woff[j] = wbase[cls];
+      rbase[cls] += n;
+      wbase[cls] += cls == 0 ? (n + 255) / 256 : 1;
+    }
+    int32_t* sm = s.summary;
+    sm[FDL_SUM_Q] = acc;
+    sm[FDL_SUM_N_MASKED_ROWS] = n_masked_rows;
+    sm[FDL_SUM_N_LONG] = cnt[0];
+    sm[FDL_SUM_N_MID] = cnt[1];
+    sm[FDL_SUM_N_SHORT] = cnt[2];
+    sm[FDL_SUM_N_CONT] = n_cont;
+    sm[FDL_SUM_N_DONE] = n_done;
+    sm[FDL_SUM_OVERFLOW] = acc > s.q_cap || cnt[0] + cnt[1] + cnt[2] > s.work_cap;
+  }
+  __syncthreads();
+  if (s.summary[FDL_SUM_OVERFLOW]) return;  // the host raises; nothing is written past a buffer
+  for (int j = wave; j < B; j += kSchedWaves) {
+    if (s_roff[j] < 0) continue;
+    const int32_t* q = seq_of(s, j);
+    const int nd = q[FDL_SEQ_ND], nm = q[FDL_SEQ_N_MASKED], nt = q[FDL_SEQ_N_TRACKED];
+    const int t0 = q[FDL_SEQ_T0], n1 = nd - t0;
+    const int64_t* fp = s.full_pos + j * L;
+    for (int i = lane; i < nm; i += kWave) {
+      const int64_t p = fp[nd + i];
+      s.qpos[s_moff[j] + i] = p;
+      s.xq[s_moff[j] + i] = s.x[p];
+      s.row_idx[s_roff[j] + i] = s_moff[j] + i;
+    }
+    for (int i = lane; i < nt; i += kWave) {
+      const int64_t p = i < n1 ? fp[t0 + i] : fp[nd + bm + (i - n1)];
+      s.qpos[s_toff[j] + i] = p;
+      s.xq[s_toff[j] + i] = s.x[p];
+      s.row_idx[s_roff[j] + nm + i] = s_toff[j] + i;
+    }
+    const int n = nm + nt;
+    const int chunk = n <= 128 ? n : 256;
+    for (int c = lane; c * chunk < n; c += kWave) {
+      int32_t* w = s.work + 8 * (s_woff[j] + c);
+      const int r0 = c * chunk, nr = n - r0 < chunk ? n - r0 : chunk;
+      w[0] = j;
+      w[1] = 0;
+      w[2] = q[FDL_SEQ_SEQLEN_K];
+      w[3] = s_roff[j] + r0;
+      w[4] = nr;
+      w[5] = c == 0 ? nm : 0;  // the masked rows feed the importance (first tile)
+      w[6] = 0;
+      w[7] = 0;
+    }
+  }
+}
+
+int check_sched(const char* fn, const fdl_sched* s) {
+  FDL_REQUIRE(s != nullptr, FDL_ERR_NULL, "%s: state is NULL", fn);
+  FDL_REQUIRE(s->n_seq >= 1 && s->n_seq <= kMaxSeq, FDL_ERR_UNSUPPORTED,
+              "%s: n_seq = %lld outside [1, %d]", fn, (long long)s->n_seq, kMaxSeq);
+  FDL_REQUIRE(s->block_m >= 2 && s->block_m <= kMaxBm, FDL_ERR_UNSUPPORTED,
+              "%s: block_m = %d outside [2, %d]", fn, s->block_m, kMaxBm);
+  FDL_REQUIRE(s->max_length >= s->block_m && s->n_seq * s->max_length < (int64_t(1) << 31),
+              FDL_ERR_SHAPE, "%s: max_length = %lld out of range", fn, (long long)s->max_length);
+  FDL_REQUIRE(s->x && s->x_draft && s->full_pos && s->seq && s->summary, FDL_ERR_NULL,
+              "%s: a state array is NULL", fn);
+  return FDL_OK;
+}
+
+}  // namespace
+}  // namespace fdl
+
+extern "C" int fdl_sched_pass1(const fdl_sched* state, const double* conf, const int64_t* tok,
+                               void* stream) {
+  using namespace fdl;
+  int rc = check_sched("fdl_sched_pass1", state);
+  if (rc != FDL_OK) return rc;
+  FDL_REQUIRE(state->seg != nullptr, FDL_ERR_NULL, "fdl_sched_pass1: seg is NULL");
+  FDL_REQUIRE(!state->verify || (state->vpos && state->xv && state->key_pos && state->vblocks &&
+                                 state->vmeta && state->draft_tok),
+              FDL_ERR_NULL, "fdl_sched_pass1: a verify list is NULL");
+  hipLaunchKernelGGL(sched_pass1_kernel, dim3(1), dim3(kSchedThreads), 0,
+                     static_cast<hipStream_t>(stream), *state, conf, tok);
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}
+
+extern "C" int fdl_sched_verify_accept(const fdl_sched* state, const double* prob, void* stream) {
+  using namespace fdl;
+  int rc = check_sched("fdl_sched_verify_accept", state);
+  if (rc != FDL_OK) return rc;
+  FDL_REQUIRE(state->seg != nullptr && prob != nullptr, FDL_ERR_NULL,
+              "fdl_sched_verify_accept: seg or prob is NULL");
+  hipLaunchKernelGGL(sched_verify_kernel, dim3(1), dim3(kSchedThreads), 0,
+                     static_cast<hipStream_t>(stream), *state, prob);
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}
+
+extern "C" int fdl_sched_pack(const fdl_sched* state, void* stream) {
+  using namespace fdl;
+  int rc = check_sched("fdl_sched_pack", state);
+  if (rc != FDL_OK) return rc;
+  FDL_REQUIRE(state->qpos && state->xq && state->row_idx && state->work, FDL_ERR_NULL,
+              "fdl_sched_pack: a step buffer is NULL");
+  FDL_REQUIRE(state->q_cap >= 0 && state->work_cap >= 0, FDL_ERR_SHAPE,
+              "fdl_sched_pack: q_cap = %lld, work_cap = %lld", (long long)state->q_cap,
+              (long long)state->work_cap);
+  hipLaunchKernelGGL(sched_pack_kernel, dim3(1), dim3(kSchedThreads), 0,
+                     static_cast<hipStream_t>(stream), *state);
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}

@@ -99,6 +99,7 @@ class DecodeStats:
     rows: int = 0
     verify_accepted: int = 0  # tokens accepted by the verify pass
     decoded: int = 0          # tokens decoded (both passes), finished or not
+    host_syncs: int = 0        # host waits for the GPU (device-scheduled decode)
     fused_rank_steps: int = 0  # steps whose ranking folded in the last layer's reduction
     split_rank_steps: int = 0  # steps that reduced first (a ranked row without importance)
     wall_s: float = 0.0
@@ -163,13 +164,16 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                              verify=False, sliding_window=True, is_instruct=True, tokenizer=None,
                              stop_tokens=None, stats: DecodeStats | None = None, use_gpu_rank: bool = True,
                              rows_only: bool = True, max_steps: int | None = None,
-                             kv_pages: int | None = None):
+                             kv_pages: int | None = None, device_schedule: bool = False):
     """Returns (responses, num_tokens, max_num_tokens) like llada/generate.py:472.
 
     use_gpu_rank: rank the decoded slots with fdl_importance_rank (else numpy, same order).
     rows_only: run the LM head only on the rows the step reads (else on every row).
     max_steps: stop after this many denoising steps (benchmarking a bounded sample;
         stats.decoded then counts the tokens decoded so far).
+    device_schedule: keep the decode's bookkeeping on the device (fdl.device_decode; one
+        host synchronisation per step). Needs the HIP driver on a GPU, the fixed-stride layout,
+        the device ranking and no tokenizer; the decisions are the same.
     kv_pages: K/V caches as a pool of this many 32-slot pages (None: the fixed stride of L
         slots per sequence). A sequence starts with the pages of its seqlen_k key slots and
         gets more when its masked block reaches past them; admission reserves pages up to
@@ -183,12 +187,22 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     """
     dev = model.device
     cfg = model.config
+    stats = stats if stats is not None else DecodeStats()
+    if device_schedule:
+        if (torch.device(dev).type != "cuda" or kv_pages is not None or tokenizer is not None
+                or not use_gpu_rank or not rows_only or not _accepts_logit_rows(model)):
+            raise ValueError("device_schedule needs a GPU model with logit rows, the fixed-stride "
+                             "cache layout, the device ranking and no tokenizer")
+        from .device_decode import generate_device_scheduled
+        return generate_device_scheduled(model, prompts, prompt_lengths, batch_size, responses,
+                                         n_steps, gen_length, block_length, mask_id, threshold,
+                                         gamma, track_num, mask_num, eos_id, verify, stats,
+                                         max_steps)
     bm = block_length
     bn = 128
     B = batch_size
     L = ((max(prompt_lengths) + gen_length + bm) // bn + 1) * bn
     d_model, n_layers, n_heads = cfg.d_model, cfg.n_layers, cfg.n_heads
-    stats = stats if stats is not None else DecodeStats()
     rows_only = rows_only and _accepts_logit_rows(model)
     row_kw = (lambda rows: {"logit_rows": rows}) if rows_only else (lambda rows: {})
     t_start = time.perf_counter()
@@ -492,17 +506,22 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             if gpu_rank:
                 enqueue_rank()
             vq = np.concatenate([seqs[j].verify_pos for j in range(B) if active[j] != -1])
-            # only the mask-view rows [T+S, T+2S) of each block are read (:318)
-            lr = np.concatenate([np.arange(a + T + S, a + T + 2 * S) for (a, T, S) in verify_meta.values()])
-            draft_rows = np.concatenate([np.arange(a + T, a + T + S) for (a, T, S) in verify_meta.values()])
+            # the mask-view rows [T+S, T+2S) of each block are read (:318); the LM head runs on
+            # the block's last block_m // 2 rows, which hold them (the last S), so every block
+            # gives the product the same number of rows whatever its S
+            tail = bm // 2
+            lr = np.concatenate([np.arange(a + 2 * bm - tail, a + 2 * bm) for (a, T, S) in verify_meta.values()])
             xv = np.concatenate(x_verify)
+            tail_tok = np.concatenate([np.where(np.arange(tail) >= tail - S,
+                                                xv[np.clip(a + T + np.arange(tail) - (tail - S), a, None)], -1)
+                                       for (a, T, S) in verify_meta.values()])
             vblocks_d, key_pos_d, mask_d, vq_d, xq, lr_d, draft_tok = _to_dev_many(
                 [np.asarray(vblocks, np.int32), phys(np.concatenate(key_pos).astype(np.int64)),
-                 np.concatenate(masks), vq, xv, lr.astype(np.int64), xv[draft_rows]], dev)
+                 np.concatenate(masks), vq, xv, lr.astype(np.int64), tail_tok.astype(np.int64)], dev)
             xq = xq[None]
             positions = [vq_d, key_pos_d, rope, None, attn_scores, mask_d]
             lengths = [start_layer, vblocks_d, None, tb_t, None, active, len(mb), L, bm, bn, None, True]
-            if len(lr):
+            if any(S for (_, _, S) in verify_meta.values()):
                 vlog = model(xq, use_cache=True, lengths=lengths, positions=positions,
                              **row_kw(lr_d)).logits.squeeze(0)
                 if not rows_only:
@@ -512,19 +531,21 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 if vlog.dtype == torch.bfloat16 and vlog.is_cuda:
                     pv = ops.softmax_confidence(vlog.contiguous(), draft_tok)[0]
                 else:
-                    pv = F.softmax(vlog.to(torch.float64), dim=-1).gather(1, draft_tok[:, None]).view(-1)
+                    pv = F.softmax(vlog.to(torch.float64), dim=-1).gather(
+                        1, draft_tok.clamp(min=0)[:, None]).view(-1)
+                    pv = torch.where(draft_tok < 0, torch.zeros_like(pv), pv)
                 pv = pv.cpu().numpy()
                 del vlog
             else:
-                pv = np.zeros(0)
+                pv = np.zeros(tail * len(verify_meta))
             off = 0
             for j, (a, T, S) in verify_meta.items():
                 s = seqs[j]
+                off += tail
                 if S == 0:
                     keep_num[j] = 0
                     continue
-                probs = pv[off:off + S].copy()
-                off += S
+                probs = pv[off - S:off].copy()
                 if s.decoded_eos != -1:
                     probs[s.verify_pos[T:T + S] >= s.predicted_length] = 0
                 cp = np.cumprod(probs)

@@ -118,10 +118,32 @@ SIGNATURES: dict[str, tuple] = {
     "fdl_split_reduce_residual": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p]),
     # logits, n_rows, vocab, token, prob, arg, stream
     "fdl_softmax_confidence": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _p, _p]),
+    # state, conf, tok, stream / state, prob, stream / state, stream
+    "fdl_sched_pass1": (ctypes.c_int, [_p, _p, _p, _p]),
+    "fdl_sched_verify_accept": (ctypes.c_int, [_p, _p, _p]),
+    "fdl_sched_pack": (ctypes.c_int, [_p, _p]),
     "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),
     "fdl_validate_work": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i64]),
     "fdl_validate_vblocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i32]),
 }
+
+# fdl_sched (include/fdl.h): device pointers, sizes and parameters of the device scheduler
+SCHED_SEQ_FIELDS = 16
+SEQ_ACTIVE, SEQ_ND, SEQ_SEQLEN_K, SEQ_PRED, SEQ_EOS, SEQ_N_MASKED, SEQ_KEEP, SEQ_T, SEQ_S, \
+    SEQ_DONE, SEQ_N_TRACKED, SEQ_T0, SEQ_T1, SEQ_FRESH, SEQ_ERR = range(15)
+SCHED_SUMMARY_FIELDS = 16
+SUM_Q, SUM_N_MASKED_ROWS, SUM_N_LONG, SUM_N_MID, SUM_N_SHORT, SUM_N_CONT, SUM_N_DONE, \
+    SUM_OVERFLOW, SUM_DECODED, SUM_VERIFY_ACCEPTED = range(10)
+
+
+class SchedState(ctypes.Structure):
+    _fields_ = [(n, _p) for n in ("x", "x_draft", "full_pos", "seq", "summary", "qpos", "xq",
+                                  "row_idx", "work", "seg", "vpos", "xv", "key_pos", "vblocks",
+                                  "vmeta", "draft_tok")] + \
+        [(n, _i64) for n in ("n_seq", "max_length", "q_cap", "work_cap")] + \
+        [(n, _i32) for n in ("block_m", "track_num", "mask_num", "verify")] + \
+        [("eos_id", _i64), ("threshold", ctypes.c_double), ("gamma", ctypes.c_double)]
+
 
 _lib: ctypes.CDLL | None = None
 

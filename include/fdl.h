@@ -294,6 +294,92 @@ int fdl_split_reduce_residual(const float* part, int64_t n_split, int64_t n_rows
 int fdl_softmax_confidence(const void* logits, int64_t n_rows, int64_t vocab,
                            const int64_t* token, double* prob, int64_t* arg, void* stream);
 
+/*
+ * Device-side decode scheduler (the bookkeeping of generate.py:125-470 in device memory; one
+ * host synchronisation per denoising step). Every pointer is device memory; the struct is
+ * read on the host at each call (pass it by host pointer).
+ *
+ * Per-sequence state seq int32 [n_seq][FDL_SCHED_SEQ_FIELDS] (field indices below); token
+ * ids x / x_draft int64 [n_seq * max_length] and the slot order full_pos int64
+ * [n_seq][max_length] hold logical slots j * max_length + p, as the reference's tensors do.
+ * A row with seq[ACTIVE] < 0 is idle. A newly admitted row has FRESH = 1, ND = its prompt
+ * length, EOS = -1, PRED = the reference's predicted_length, SEQLEN_K its key count.
+ */
+enum fdl_sched_seq_field {
+  FDL_SEQ_ACTIVE = 0,     /* prompt index, -1: idle row */
+  FDL_SEQ_ND = 1,         /* decoded count (num_decoded) */
+  FDL_SEQ_SEQLEN_K = 2,   /* keys of the sequence (seqlen_k) */
+  FDL_SEQ_PRED = 3,       /* predicted_length (a slot bound) */
+  FDL_SEQ_EOS = 4,        /* decoded_eos_pos (a slot) or -1 */
+  FDL_SEQ_N_MASKED = 5,   /* masked rows of the step: full_pos[ND : ND + N_MASKED] */
+  FDL_SEQ_KEEP = 6,       /* tokens accepted by the step's last acceptance stage */
+  FDL_SEQ_T = 7,          /* verify fill rows */
+  FDL_SEQ_S = 8,          /* verify candidates */
+  FDL_SEQ_DONE = 9,       /* 1: nothing left before the predicted length */
+  FDL_SEQ_N_TRACKED = 10, /* tracked rows: full_pos[T0 : ND] then full_pos[ND + block_m : T1] */
+  FDL_SEQ_T0 = 11,
+  FDL_SEQ_T1 = 12,
+  FDL_SEQ_FRESH = 13,     /* 1: the next step recomputes every slot (step 0 of a prompt) */
+  FDL_SEQ_ERR = 14,       /* 1: fewer decoded slots than verify fill rows */
+  FDL_SCHED_SEQ_FIELDS = 16,
+};
+/* summary int32 [FDL_SCHED_SUMMARY_FIELDS], written by fdl_sched_pack (DECODED and
+ * VERIFY_ACCEPTED are running totals the caller may reset) */
+enum fdl_sched_summary_field {
+  FDL_SUM_Q = 0,              /* packed rows of the next forward */
+  FDL_SUM_N_MASKED_ROWS = 1,  /* its first rows, the masked ones (the LM head rows) */
+  FDL_SUM_N_LONG = 2,         /* work items: long (256-row) tiles, then mid, then short */
+  FDL_SUM_N_MID = 3,
+  FDL_SUM_N_SHORT = 4,
+  FDL_SUM_N_CONT = 5,         /* active rows that continue */
+  FDL_SUM_N_DONE = 6,         /* active rows that finished (DONE = 1) */
+  FDL_SUM_OVERFLOW = 7,       /* 1: rows or items beyond q_cap / work_cap (nothing written) */
+  FDL_SUM_DECODED = 8,
+  FDL_SUM_VERIFY_ACCEPTED = 9,
+  FDL_SCHED_SUMMARY_FIELDS = 16,
+};
+typedef struct fdl_sched {
+  int64_t* x;          /* token ids */
+  int64_t* x_draft;    /* pass-1 draft tokens */
+  int64_t* full_pos;   /* slot order */
+  int32_t* seq;        /* per-sequence fields */
+  int32_t* summary;
+  /* next forward (fdl_sched_pack): packed slots and token ids, work items of
+   * fdl_block_attention (long, mid, short tiles in that order) and their row lists */
+  int64_t* qpos;       /* [q_cap] */
+  int64_t* xq;         /* [q_cap] */
+  int32_t* row_idx;    /* [q_cap] */
+  int32_t* work;       /* [work_cap][8] */
+  /* ranking segments (start, len) of the active rows, in row order (acceptance kernels) */
+  int32_t* seg;        /* [n_seq][2] */
+  /* Flash-Verify lists of the active rows (fdl_sched_pass1 with verify = 1): block a holds
+   * packed rows [2 block_m a, 2 block_m (a + 1)) */
+  int64_t* vpos;       /* [n_seq * 2 block_m] slots of the verify rows */
+  int64_t* xv;         /* [n_seq * 2 block_m] their token ids */
+  int64_t* key_pos;    /* [n_seq * max_length] cache keys of the blocks, packed */
+  int32_t* vblocks;    /* [n_seq][4] (k0, k1, q0, q1) */
+  int32_t* vmeta;      /* [n_seq][2] (T, S) */
+  int64_t* draft_tok;  /* [n_seq * block_m / 2] draft token of the last block_m / 2 rows of
+                          each block (its mask rows are the last S of them), -1 elsewhere */
+  int64_t n_seq, max_length, q_cap, work_cap;
+  int32_t block_m, track_num, mask_num, verify;
+  int64_t eos_id;
+  double threshold, gamma;
+} fdl_sched;
+
+/* Pass-1 acceptance from the masked rows' float64 confidences and tokens
+ * (fdl_softmax_confidence over the first FDL_SUM_N_MASKED_ROWS rows) and, with verify, the
+ * verify lists. Replaces generate.py:215-258 (with Flash-Verify), :335-350 (without) and
+ * :260-297. */
+int fdl_sched_pass1(const fdl_sched* state, const double* conf, const int64_t* tok,
+                    void* stream);
+/* Verify acceptance from the float64 probability of each block's draft tokens on its last
+ * block_m / 2 rows (fdl_softmax_confidence with draft_tok). Replaces generate.py:307-333. */
+int fdl_sched_verify_accept(const fdl_sched* state, const double* prob, void* stream);
+/* Completion test and the next step's masked / tracked rows, packed, with the attention
+ * work items; the summary. Replaces generate.py:364-383 (after the ranking) and :439-467. */
+int fdl_sched_pack(const fdl_sched* state, void* stream);
+
 /* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
  * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
 int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,

@@ -83,6 +83,29 @@ def test_launchers_reject_bad_scalars_without_gpu():
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_softmax_confidence", None, 4, 12, None, None, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_softmax_confidence", None, 4, 16, None, None, None, None)
     lib.call("fdl_softmax_confidence", None, 0, 16, None, None, None, None)  # zero rows: no-op
+    # scheduler state: NULL state, sizes out of range, missing arrays
+    st = lib.SchedState()
+    assert ctypes.sizeof(lib.SchedState) == 16 * 8 + 4 * 8 + 4 * 4 + 8 + 2 * 8  # fdl_sched
+    _expect(lib.FDL_ERR_NULL, "fdl_sched_pass1", None, None, None, None)
+    st.n_seq, st.block_m, st.max_length = 0, 32, 1024
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_sched_pass1", ctypes.byref(st), None, None, None)
+    st.n_seq, st.block_m = 8, 1
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_sched_pack", ctypes.byref(st), None)
+    st.block_m, st.max_length = 32, 16
+    _expect(lib.FDL_ERR_SHAPE, "fdl_sched_verify_accept", ctypes.byref(st), None, None)
+    st.max_length = 1024
+    msg = _expect(lib.FDL_ERR_NULL, "fdl_sched_pack", ctypes.byref(st), None)
+    assert "fdl_sched_pack: a state array" in msg
+    for name in ("x", "x_draft", "full_pos", "seq", "summary", "seg"):
+        setattr(st, name, 8)  # never dereferenced: rejected before any launch
+    st.verify = 1
+    assert "verify" in _expect(lib.FDL_ERR_NULL, "fdl_sched_pass1", ctypes.byref(st), None, None,
+                               None)
+    _expect(lib.FDL_ERR_NULL, "fdl_sched_verify_accept", ctypes.byref(st), None, None)
+    for name in ("qpos", "xq", "row_idx", "work"):
+        setattr(st, name, 8)
+    st.q_cap = -1
+    _expect(lib.FDL_ERR_SHAPE, "fdl_sched_pack", ctypes.byref(st), None)
     # every other entry point: an empty call returns before any pointer is read
     lib.call("fdl_importance_rank", None, 10, None, 10, None, 0, 16, None, 0, None)
     lib.call("fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 5, None, None, 10,

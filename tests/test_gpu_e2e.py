@@ -284,3 +284,35 @@ def test_paged_pool_decode_matches_fixed_stride_on_gpu(verify):
                                            stats=st, kv_pages=pages, **kw)
         out.append((r, n, m, st.steps, st.forwards))
     assert out[0] == out[1]
+
+
+@pytest.mark.parametrize("verify,block,lengths", [
+    (False, 32, [96, 128, 100, 72, 80]),
+    (True, 32, [96, 128, 100, 72, 80]),
+    (True, 16, [96, 128, 100, 72, 80]),
+    (True, 64, [130, 160, 140, 135, 150]),
+])
+def test_device_schedule_matches_host_schedule(verify, block, lengths):
+    """The decode with its bookkeeping on the device (fdl_sched_* kernels: pass-1 and verify
+    acceptance, verify lists and closed-form mask, next-step packing; ranking in place)
+    gives the host-scheduled decode token for token, with the same token counts and
+    per-prompt step counts; 5 prompts through 3 rows (refills). One host synchronisation per
+    step, plus one at start and one per admitted prompt."""
+    model = _model(lm_head_std=1.0, seed=2)
+    rng = np.random.default_rng(9)
+    prompts = [torch.from_numpy(rng.integers(0, 2000, n)) for n in lengths]
+    kw = dict(gen_length=96, block_length=block, mask_id=2046, threshold=0.9, gamma=0.9,
+              track_num=1, mask_num=1, eos_id=2045, verify=verify)
+    out = []
+    for device_schedule in (False, True):
+        st = DecodeStats()
+        steps = [0] * 5
+        r, n, m = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, steps, stats=st,
+                                           device_schedule=device_schedule, **kw)
+        out.append((r, n, m, steps, st))
+    (r_h, n_h, m_h, s_h, st_h), (r_d, n_d, m_d, s_d, st_d) = out
+    print(f"verify={verify} block={block}: {st_d.steps} steps, {st_d.host_syncs} host syncs "
+          f"(device), decoded {st_d.decoded}, verify accepted {st_d.verify_accepted}")
+    assert r_d == r_h and n_d == n_h and m_d == m_h and s_d == s_h
+    assert st_d.steps == st_h.steps and st_d.decoded == st_h.decoded
+    assert st_d.host_syncs <= st_d.steps + 1 + 5
