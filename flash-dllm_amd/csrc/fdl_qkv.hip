@@ -14,18 +14,19 @@
 // computes both members of its pairs, so lane l holds (c, c + 64) of the same rows in the
 // same accumulator slot and RoPE runs in registers before the bf16 stores.
 //
-// Two kernels, chosen by the number of rows:
-//  * qkv_pc_kernel (more than 64 rows): 128 rows x 96 pairs per workgroup (512 rows: one
-//    tile per CU). Sixteen wavefronts in two roles: four producers move the X and W tiles
-//    of each 64-wide reduction step straight from global memory into LDS (global_load_lds,
-//    three LDS stages in flight), and twelve consumers (three per SIMD) run the 16x16x32
-//    MFMAs from LDS. A consumer never issues a global memory instruction, so it is never
-//    held behind the texture-address queue, and the three consumers of a SIMD hide each
-//    other's LDS latency.
-//  * qkv_stream_kernel<BM, BP> (up to 64 rows, weight streaming): 64 rows x 32 pairs per
-//    workgroup so the launch covers the CUs; X and W tiles staged through LDS with the
-//    global loads kStages steps ahead in a ring of registers and the LDS fragment reads of
-//    the next half-step interleaved with the MFMAs of the current one.
+// One kernel, qkv_pc_kernel<BM, BP, NPROD, STAGES>: a workgroup computes BM rows x BP pairs
+// with wavefronts in two roles. NPROD producers move the X and W tiles of each 64-wide
+// reduction step straight from global memory into LDS (global_load_lds), STAGES steps deep;
+// four consumers (one per SIMD, a 2 x 2 grid over rows and pairs) run the 16x16x32 MFMAs
+// from LDS. A consumer never issues a global memory instruction, so its MFMA stream is
+// never held behind the texture-address queue. After the reduction the consumers stage the
+// fp32 sums in the (then free) stage memory and every wavefront rotates and writes 8-pair
+// groups with 16-byte stores. Two shapes, chosen by the number of rows:
+//  * more than 128 rows: 128 rows x 96 pairs, 4 stages of 40 KB (all of LDS). 512 rows give
+//    one tile per CU.
+//  * up to 128 rows (weight streaming, HBM-bound): 64 or 128 rows x 32 pairs (192 tiles at
+//    d_model 4096), 8 stages of 16 KB or 6 of 24 KB, so each workgroup keeps 5-7 weight
+//    steps in flight.
 #include <atomic>
 #include <type_traits>
 
@@ -38,8 +39,7 @@ namespace {
 constexpr int kHeadDim = 128;
 constexpr int kHalf = 64;
 constexpr int kKT = 64;  // reduction step, bf16 elements (8 chunks of 16 B per row)
-constexpr int kThreads = 256;
-constexpr int kStages = 4;  // reduction steps in flight (register ring); even
+constexpr int kDAlign = 256;  // d_model must be a multiple of this
 
 struct QkvArgs {
   const uint16_t* x;
@@ -61,10 +61,9 @@ struct QkvArgs {
   int kv_packed;
 };
 
-// Chunk c (16 B) of LDS row r is stored at chunk c ^ ((r >> 1) & 7) of that row: two
-// 128-byte rows share one 256-byte bank line, so 16 consecutive rows read at the same
-// logical chunk land on 16 distinct 4-bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+// LDS tile layout: chunk c (16 B) of tile row r is stored at chunk c ^ ((r >> 1) & 7) of
+// that row: two 128-byte rows share one 256-byte bank line, so 16 consecutive rows read at
+// the same logical chunk land on 16 distinct 4-bank groups.
 
 // Workgroup i runs on XCD i % 8. Renumber so that each XCD gets a contiguous run of tiles
 // (tiles are numbered n-block-major): the m-tiles that share one weight slice then run on
@@ -87,240 +86,94 @@ __device__ __forceinline__ void tile_coords(int t, int n_mtiles, int n_tiles, in
   mt = grp * kGroupM + (r - nt * gm);
 }
 
-// Destination rows of tile rows m0 .. m0 + BM - 1, written by threads 0 .. BM - 1:
-// dst[0] = Q row, dst[1] = K/V row (cache slot, or the packed row), rope = sin/cos row.
-// A row past n_rows, or with an out-of-range slot or rope row, gets -1 (skipped in all
-// three outputs).
-template <int BM>
-__device__ __forceinline__ void tile_rows(const QkvArgs& a, int64_t m0, int64_t (&dst)[2][BM],
-                                          int64_t (&rope)[BM]) {
-  const int tid = threadIdx.x;
-  if (tid < BM) {
-    const int64_t r = m0 + tid;
-    int64_t dq = -1, dkv = -1, rr_ok = -1;
-    if (r < a.n_rows) {
-      const int64_t s = a.slot[r];
-      const int64_t rr = a.rope_row ? a.rope_row[r] : s;
-      const bool rope_ok = rr >= 0 && rr < a.n_rope_rows;
-      const bool slot_ok = a.kv_packed || (s >= 0 && s < a.n_kv_rows);
-      if (rope_ok && slot_ok) {
-        dq = r;
-        dkv = a.kv_packed ? r : s;
-        rr_ok = rr;
-      }
+// Destinations of row r: dq = Q row, dkv = K/V row (cache slot, or the packed row), rope =
+// sin/cos row. A row past n_rows, or with an out-of-range slot or rope row, gets -1 in all
+// three (skipped in all three outputs).
+__device__ __forceinline__ void row_dest(const QkvArgs& a, int64_t r, int64_t& dq, int64_t& dkv,
+                                         int64_t& rope) {
+  dq = dkv = rope = -1;
+  if (r < a.n_rows) {
+    const int64_t s = a.slot[r];
+    const int64_t rr = a.rope_row ? a.rope_row[r] : s;
+    const bool rope_ok = rr >= 0 && rr < a.n_rope_rows;
+    const bool slot_ok = a.kv_packed || (s >= 0 && s < a.n_kv_rows);
+    if (rope_ok && slot_ok) {
+      dq = r;
+      dkv = a.kv_packed ? r : s;
+      rope = rr;
     }
-    dst[0][tid] = dq;
-    dst[1][tid] = dkv;
-    rope[tid] = rr_ok;
   }
 }
 
-// Rotates (lo, hi) = (q~_c, q~_{c+64}) of one row and stores the bf16 pair.
-__device__ __forceinline__ void store_pair(const QkvArgs& a, int mat, int64_t dst, int64_t rope,
-                                           int head, int c, float lo, float hi) {
-  if (mat < 2) {
-    const float* sn = a.sin + rope * kHeadDim;
-    const float* cs = a.cos + rope * kHeadDim;
-    const float s1 = sn[c], s2 = sn[c + kHalf], c1 = cs[c], c2 = cs[c + kHalf];
-    const float rlo = lo * c1 - hi * s1;
-    const float rhi = hi * c2 + lo * s2;
-    lo = rlo;
-    hi = rhi;
-  }
-  uint16_t* base = mat == 0 ? a.q_out : (mat == 1 ? a.k_out : a.v_out);
-  uint16_t* d = base + dst * a.d_model + int64_t(head) * kHeadDim;
-  d[c] = f2bf(lo);
-  d[c + kHalf] = f2bf(hi);
-}
+// 8 consecutive pairs (c0 .. c0 + 7 of one head; lo = q~_c, hi = q~_{c+64}) of one row:
+// load() reads the fp32 sums from LDS and the sin/cos values, store() rotates and writes two
+// 16-byte bf16 chunks. c0 is a multiple of 8, so the sin/cos reads and both stores are
+// 16-byte aligned. A group whose row has no destination (dst < 0) reads and writes nothing.
+struct EpGroup {
+  f32x4 lo[2], hi[2];
+  f32x4 s1[2], s2[2], c1[2], c2[2];
+  int64_t dst;
+  int mat, head, c0;
 
-// ---------------------------------------------------------------------------------------
-// qkv_stream_kernel: BM rows x BP pairs per workgroup; wavefront (wm, wn) owns rows
-// BM/2 * wm .. + BM/2 and pairs BP/2 * wn .. + BP/2 (low and high columns).
-template <int BM, int BP, int OCC>
-__global__ __launch_bounds__(kThreads, OCC) void qkv_stream_kernel(QkvArgs a) {
-  constexpr int kWP = BP / 2;               // pairs per wavefront
-  constexpr int kPB = kWP / 16;             // 16-pair MFMA blocks per wavefront
-  constexpr int kRB = BM / 32;              // 16-row MFMA blocks per wavefront
-  constexpr int kXLd = BM * 8 / kThreads;   // X chunks per thread per step
-  constexpr int kWLd = 2 * BP * 8 / kThreads;  // W chunks per thread per step
-  static_assert(kPB >= 1 && kRB >= 1 && kXLd >= 1 && kWLd >= 1, "tile too small");
-  __shared__ u32x4 As[2][BM * 8];
-  __shared__ u32x4 Bs[2][2 * BP * 8];  // rows 0 .. BP-1: low columns; BP .. 2BP-1: high
-  __shared__ int64_t s_dst[2][BM];
-  __shared__ int64_t s_rope[BM];
-
-  const int tid = threadIdx.x;
-  int nt, mt;
-  tile_coords(xcd_tile(blockIdx.x, a.n_tiles), a.n_mtiles, a.n_tiles, nt, mt);
-  const int64_t m0 = int64_t(mt) * BM;
-  const int D = a.d_model;
-  const int pairs_per_mat = a.n_heads * kHalf;
-  tile_rows<BM>(a, m0, s_dst, s_rope);
-
-  // Global -> LDS staging sources. Tile rows past n_rows load row n_rows - 1 (never
-  // stored), so every load is unconditional and the compiler's wait counts stay exact.
-  const uint16_t* xsrc[kXLd];
-  const uint16_t* wsrc[kWLd];
-  int xdst[kXLd], wdst[kWLd];
+  __device__ __forceinline__ void load(const QkvArgs& a, const float* src, int hi_off, int m,
+                                       int rem, int64_t d, int64_t rope) {
+    mat = m;
+    head = rem >> 6;
+    c0 = rem & 63;
+    dst = d;
+    if (d < 0) return;
+    lo[0] = *reinterpret_cast<const f32x4*>(src);
+    lo[1] = *reinterpret_cast<const f32x4*>(src + 4);
+    hi[0] = *reinterpret_cast<const f32x4*>(src + hi_off);
+    hi[1] = *reinterpret_cast<const f32x4*>(src + hi_off + 4);
+    if (m < 2) {
+      const float* sn = a.sin + rope * kHeadDim + c0;
+      const float* cs = a.cos + rope * kHeadDim + c0;
 #pragma unroll
-  for (int i = 0; i < kXLd; ++i) {
-    const int id = tid + kThreads * i, row = id >> 3, c = id & 7;
-    const int64_t r = min(m0 + row, a.n_rows - 1);
-    xsrc[i] = a.x + r * D + 8 * c;
-    xdst[i] = swz(row, c);
-  }
-#pragma unroll
-  for (int i = 0; i < kWLd; ++i) {
-    const int id = tid + kThreads * i, row = id >> 3, c = id & 7;
-    const int hlf = row / BP, p = BP * nt + (row - hlf * BP);
-    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
-    wsrc[i] = a.w[mat] + int64_t((rem >> 6) * kHeadDim + (rem & 63) + kHalf * hlf) * D + 8 * c;
-    wdst[i] = swz(row, c);
-  }
-  struct Stage {
-    u32x4 x[kXLd], w[kWLd];
-  };
-  Stage ring[kStages];
-  const int nk = D / kKT;  // a multiple of kStages (checked on the host)
-  // Steps past the end re-read the last step (never committed).
-  auto issue = [&](Stage& st, int kt) {
-    const int k0 = min(kt, nk - 1) * kKT;
-#pragma unroll
-    for (int i = 0; i < kXLd; ++i) st.x[i] = ld16(xsrc[i] + k0);
-#pragma unroll
-    for (int i = 0; i < kWLd; ++i) st.w[i] = ld16(wsrc[i] + k0);
-  };
-  auto commit = [&](const Stage& st, int buf) {
-#pragma unroll
-    for (int i = 0; i < kXLd; ++i) As[buf][xdst[i]] = st.x[i];
-#pragma unroll
-    for (int i = 0; i < kWLd; ++i) Bs[buf][wdst[i]] = st.w[i];
-  };
-
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l16 = lane & 15, g4 = lane >> 4;
-  // MFMA operands of one 32-wide half-step ss of a step: lane (l16, g4) takes chunk
-  // 4 * ss + g4 of its row.
-  struct Frag {
-    bf16x8 a[kRB];
-    bf16x8 b[2][kPB];
-  };
-  auto read_frag = [&](Frag& f, int buf, int ss) {
-    const int c = 4 * ss + g4;
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-      f.a[rb] = as_bf16x8(As[buf][swz((BM / 2) * wm + 16 * rb + l16, c)]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int pb = 0; pb < kPB; ++pb)
-        f.b[h][pb] = as_bf16x8(Bs[buf][swz(BP * h + kWP * wn + 16 * pb + l16, c)]);
-  };
-  f32x4 acc[kRB][2][kPB];
-#pragma unroll
-  for (int rb = 0; rb < kRB; ++rb)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const Frag& f) {
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int pb = 0; pb < kPB; ++pb)
-          acc[rb][h][pb] = mfma16(f.a[rb], f.b[h][pb], acc[rb][h][pb]);
-  };
-  // Instruction groups for one half-step: the LDS fragment reads and the LDS writes (first
-  // half) or global loads (second half) are spread between the MFMAs.
-  constexpr int kMfma = 2 * kRB * kPB;
-  constexpr int kMem = kXLd + kWLd;
-  auto interleave = [&](auto mem_mask) {
-    if constexpr (kMfma >= 2 * kMem) {
-#pragma unroll
-      for (int i = 0; i < kMem; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(decltype(mem_mask)::value, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      for (int h = 0; h < 2; ++h) {
+        s1[h] = *reinterpret_cast<const f32x4*>(sn + 4 * h);
+        s2[h] = *reinterpret_cast<const f32x4*>(sn + kHalf + 4 * h);
+        c1[h] = *reinterpret_cast<const f32x4*>(cs + 4 * h);
+        c2[h] = *reinterpret_cast<const f32x4*>(cs + kHalf + 4 * h);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, kMfma - 2 * kMem, 0);
-    }
-  };
-
-  Frag f0, f1;
-#pragma unroll
-  for (int s = 0; s < kStages; ++s) {
-    issue(ring[s], s);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  commit(ring[0], 0);
-  __syncthreads();
-  read_frag(f0, 0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  issue(ring[0], kStages);
-  __builtin_amdgcn_sched_barrier(0);
-  // Step kt: f0 holds half-step 0 (read earlier), LDS buffer kt & 1 holds the step, ring
-  // slot (kt + 1) % kStages holds step kt + 1 in registers.
-  for (int kt0 = 0; kt0 < nk; kt0 += kStages) {
-#pragma unroll
-    for (int j = 0; j < kStages; ++j) {
-      const int kt = kt0 + j;
-      const int buf = j & 1;  // kStages is even
-      // half-step 0: read half-step 1, store step kt + 1 to the other buffer (its last
-      // reads were before the previous barrier), MFMAs of half-step 0
-      read_frag(f1, buf, 1);
-      commit(ring[(j + 1) % kStages], buf ^ 1);
-      mma(f0);
-      interleave(std::integral_constant<int, 0x200>{});  // LDS write
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();
-      // half-step 1: read half-step 0 of step kt + 1, refill the ring slot, MFMAs
-      read_frag(f0, buf ^ 1, 0);
-      issue(ring[(j + 1) % kStages], kt + 1 + kStages);
-      mma(f1);
-      interleave(std::integral_constant<int, 0x020>{});  // global load
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // Epilogue: acc[rb][h][pb][i] is row BM/2 * wm + 16 rb + 4 g4 + i, pair
-  // BP * nt + kWP * wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
+  __device__ __forceinline__ void store(const QkvArgs& a) {
+    if (dst < 0) return;
+    float l[8], r[8];
 #pragma unroll
-  for (int pb = 0; pb < kPB; ++pb) {
-    const int p = BP * nt + kWP * wn + 16 * pb + l16;
-    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
+    for (int j = 0; j < 8; ++j) {
+      l[j] = lo[j >> 2][j & 3];
+      r[j] = hi[j >> 2][j & 3];
+    }
+    if (mat < 2) {
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (BM / 2) * wm + 16 * rb + 4 * g4 + i;
-        const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
-        if (dst < 0) continue;
-        store_pair(a, mat, dst, s_rope[row], rem >> 6, rem & 63, acc[rb][0][pb][i],
-                   acc[rb][1][pb][i]);
+      for (int j = 0; j < 8; ++j) {
+        const int h = j >> 2, e = j & 3;
+        const float rlo = l[j] * c1[h][e] - r[j] * s1[h][e];
+        const float rhi = r[j] * c2[h][e] + l[j] * s2[h][e];
+        l[j] = rlo;
+        r[j] = rhi;
       }
+    }
+    const u32x4 wlo = {pack_bf16x2(l[0], l[1]), pack_bf16x2(l[2], l[3]), pack_bf16x2(l[4], l[5]),
+                       pack_bf16x2(l[6], l[7])};
+    const u32x4 whi = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                       pack_bf16x2(r[6], r[7])};
+    uint16_t* base = mat == 0 ? a.q_out : (mat == 1 ? a.k_out : a.v_out);
+    uint16_t* d = base + dst * a.d_model + int64_t(head) * kHeadDim + c0;
+    st16(d, wlo);
+    st16(d + kHalf, whi);
   }
-}
-
-// ---------------------------------------------------------------------------------------
-// qkv_pc_kernel: 128 rows x 96 pairs; consumer wavefront (wm, wn), wm < 4, wn < 3, owns rows
-// 32 wm .. + 32 and pairs 32 wn .. + 32 (low and high columns).
-constexpr int kPcBM = 128;
-constexpr int kPcBP = 96;
-constexpr int kPcThreads = 1024;  // 12 consumer + 4 producer wavefronts
-constexpr int kPcStages = 3;                         // LDS stages
-constexpr int kPcABytes = kPcBM * 128;               // X tile of one step (16 KB)
-constexpr int kPcStageBytes = kPcABytes + 2 * kPcBP * 128;  // + W tile (24 KB)
-constexpr int kPcLoads = kPcStageBytes / 1024 / 4;   // 1 KB loads per producer per step
+};
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(1))) void* glb_ptr;
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 // Workgroup barrier without the compiler's memory fence; each side waits for exactly the
@@ -330,43 +183,73 @@ __device__ __forceinline__ void barrier_lds_drained() {
 }
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
-  constexpr int kWP = kPcBP / 3, kPB = kWP / 16;
-  __shared__ __align__(1024) uint8_t smem[kPcStages * kPcStageBytes];
-  __shared__ int64_t s_dst[2][kPcBM];
-  __shared__ int64_t s_rope[kPcBM];
+// ---------------------------------------------------------------------------------------
+// Shape of one qkv_pc_kernel instance. Consumer (wm, wn), wm, wn < 2, owns rows
+// BM/2 * wm .. + BM/2 and pairs BP/2 * wn .. + BP/2 (low and high columns).
+template <int BM, int BP, int NPROD, int STAGES>
+struct PcShape {
+  static constexpr int kConsumers = 4;
+  static constexpr int kThreads = (kConsumers + NPROD) * 64;
+  static constexpr int kWP = BP / 2, kPB = kWP / 16, kRB = BM / 32;
+  static constexpr int kABytes = BM * 128;                 // X tile of one step
+  static constexpr int kStageBytes = kABytes + 2 * BP * 128;  // + W tile (low, high columns)
+  static constexpr int kLoads = kStageBytes / 1024 / NPROD;   // 1 KB loads per producer/step
+  // Epilogue staging in the stage memory once the reduction is done: the fp32 sums as rows
+  // of [BP low | BP high] columns (row stride padded by 4 floats), then the rows'
+  // destinations (Q row, K/V row, sin/cos row).
+  static constexpr int kEpStride = 2 * BP + 4;
+  static constexpr int kEpMetaOff = BM * kEpStride * 4;
+  static_assert(kPB >= 1 && kRB >= 1 && kPB * 16 == kWP && kRB * 32 == BM, "tile shape");
+  static_assert(kLoads * NPROD * 1024 == kStageBytes, "producer split");
+  static_assert((STAGES - 1) * kLoads < 64, "vmcnt range");
+  static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS");
+  static_assert(kEpMetaOff + 3 * BM * 8 <= STAGES * kStageBytes, "epilogue staging");
+  static_assert(BM <= kThreads, "row destinations");
+};
+
+template <int BM, int BP, int NPROD, int STAGES>
+__global__ __launch_bounds__((4 + NPROD) * 64, 1) void qkv_pc_kernel(QkvArgs a) {
+  using Sh = PcShape<BM, BP, NPROD, STAGES>;
+  constexpr int kWP = Sh::kWP, kPB = Sh::kPB, kRB = Sh::kRB, kLoads = Sh::kLoads;
+  constexpr int kStageBytes = Sh::kStageBytes, kEpStride = Sh::kEpStride;
+  constexpr int kThreads = Sh::kThreads, kConsumers = Sh::kConsumers;
+  __shared__ __align__(1024) uint8_t smem[STAGES * kStageBytes];
 
   const int tid = threadIdx.x;
   int nt, mt;
   tile_coords(xcd_tile(blockIdx.x, a.n_tiles), a.n_mtiles, a.n_tiles, nt, mt);
-  const int64_t m0 = int64_t(mt) * kPcBM;
+  const int64_t m0 = int64_t(mt) * BM;
   const int D = a.d_model;
   const int pairs_per_mat = a.n_heads * kHalf;
-  tile_rows<kPcBM>(a, m0, s_dst, s_rope);
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
-  // wavefront executes only its own role's barriers (both roles execute 1 + nk of them).
+  // wavefront executes only its own role's barriers (both roles execute 3 + nk of them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const bool producer = wave >= 12;
-  const int pw = wave - 12;
+  const bool producer = wave >= kConsumers;
   const int nk = D / kKT;
 
+  // Destinations of tile rows 0 .. BM - 1 (threads 0 .. BM - 1), read now and staged in LDS
+  // for the epilogue once the stage memory is free.
+  int64_t my_dq = -1, my_dkv = -1, my_rope = -1;
+  if (tid < BM) row_dest(a, m0 + tid, my_dq, my_dkv, my_rope);
+
   if (producer) {
+    const int pw = wave - kConsumers;
     // Load i of producer pw fills LDS bytes [1024 q, 1024 q + 1024) of the step's tile
     // (q = 8-row block): lane -> row 8 q + lane / 8, LDS chunk lane % 8, which holds the
-    // row's logical chunk (lane % 8) ^ ((row >> 1) & 7) (the swz() layout). Tile rows past
+    // row's logical chunk (lane % 8) ^ ((row >> 1) & 7) (the LDS tile layout). Tile rows past
     // n_rows re-read row n_rows - 1 (never stored).
-    const uint16_t* src[kPcLoads];
-    int dst_off[kPcLoads];
+    const uint16_t* src[kLoads];
+    int dst_off[kLoads];
 #pragma unroll
-    for (int i = 0; i < kPcLoads; ++i) {
-      const int q = kPcLoads * pw + i;
+    for (int i = 0; i < kLoads; ++i) {
+      const int q = kLoads * pw + i;
       const int row = 8 * q + (lane >> 3);
       const int c = (lane & 7) ^ ((row >> 1) & 7);
-      if (row < kPcBM) {
+      if (row < BM) {
         src[i] = a.x + min(m0 + row, a.n_rows - 1) * D + 8 * c;
       } else {
-        const int wr = row - kPcBM, hlf = wr / kPcBP;
-        const int p = kPcBP * nt + (wr - hlf * kPcBP);
+        const int wr = row - BM, hlf = wr / BP;
+        const int p = BP * nt + (wr - hlf * BP);
         const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
         src[i] = a.w[mat] + int64_t((rem >> 6) * kHeadDim + (rem & 63) + kHalf * hlf) * D +
                  8 * c;
@@ -376,110 +259,139 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
     // Steps past the end re-read the last step into a stage nobody reads any more.
     auto issue = [&](int kt, int stage) {
       const int k0 = min(kt, nk - 1) * kKT;
-      uint8_t* st = smem + stage * kPcStageBytes;
+      uint8_t* st = smem + stage * kStageBytes;
 #pragma unroll
-      for (int i = 0; i < kPcLoads; ++i)
+      for (int i = 0; i < kLoads; ++i)
         __builtin_amdgcn_global_load_lds((glb_ptr)(src[i] + k0), (lds_ptr)(st + dst_off[i]), 16,
                                          0, 0);
     };
-    issue(0, 0);
-    issue(1, 1);
-    issue(2, 2);
-    wait_vmcnt<2 * kPcLoads>();  // step 0 landed
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) issue(s, s);
+    wait_vmcnt<(STAGES - 1) * kLoads>();  // step 0 landed
     barrier_only();
     int stage = 0;
     for (int kt = 0; kt < nk; ++kt) {
-      wait_vmcnt<kPcLoads>();  // step kt + 1 landed (step kt + 2 may still be in flight)
+      // step kt + 1 landed (steps kt + 2 .. kt + STAGES - 1 may still be in flight)
+      wait_vmcnt<(STAGES - 2) * kLoads>();
       barrier_only();
-      issue(kt + kPcStages, stage);  // this stage's last reads came before the barrier
-      stage = stage == kPcStages - 1 ? 0 : stage + 1;
+      issue(kt + STAGES, stage);  // this stage's last reads came before the barrier
+      stage = stage == STAGES - 1 ? 0 : stage + 1;
     }
-    wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
-    return;
-  }
-
-  const int wm = wave / 3, wn = wave - 3 * (wave / 3);  // rows 32 wm .., pairs 32 wn ..
-  const int l16 = lane & 15, g4 = lane >> 4;
-  const int sw = (l16 >> 1) & 7;
-  struct Frag {
-    u32x4 a[2];
-    u32x4 b[2][kPB];
-  };
-  // MFMA operands of half-step ss of the step in `stage`: lane (l16, g4) takes logical chunk
-  // 4 ss + g4 of its row.
-  auto read_frag = [&](Frag& f, int stage, int ss) {
-    const u32x4* st = reinterpret_cast<const u32x4*>(smem + stage * kPcStageBytes);
-    const int c = (4 * ss + g4) ^ sw;
+    wait_vmcnt<0>();  // no load may still be writing LDS when the stages are reused
+    barrier_only();   // -> the consumers may overwrite the stages
+    barrier_only();   // <- the accumulators and destinations are staged
+  } else {
+    const int wm = wave >> 1, wn = wave & 1;  // rows BM/2 wm .., pairs BP/2 wn ..
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int sw = (l16 >> 1) & 7;
+    struct Frag {
+      u32x4 a[kRB];
+      u32x4 b[2][kPB];
+    };
+    // MFMA operands of half-step ss of the step in `stage`: lane (l16, g4) takes logical
+    // chunk 4 ss + g4 of its row.
+    auto read_frag = [&](Frag& f, int stage, int ss) {
+      const u32x4* st = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
+      const int c = (4 * ss + g4) ^ sw;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) f.a[rb] = st[(32 * wm + 16 * rb + l16) * 8 + c];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int pb = 0; pb < kPB; ++pb)
-        f.b[h][pb] = st[kPcABytes / 16 + (kPcBP * h + kWP * wn + 16 * pb + l16) * 8 + c];
-  };
-  f32x4 acc[2][2][kPB];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const Frag& f) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < kRB; ++rb) f.a[rb] = st[((BM / 2) * wm + 16 * rb + l16) * 8 + c];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int pb = 0; pb < kPB; ++pb)
-          acc[rb][h][pb] = mfma16(as_bf16x8(f.a[rb]), as_bf16x8(f.b[h][pb]), acc[rb][h][pb]);
-  };
-  // one LDS read between two MFMAs
-  auto interleave = [&]() {
+          f.b[h][pb] = st[Sh::kABytes / 16 + (BP * h + kWP * wn + 16 * pb + l16) * 8 + c];
+    };
+    f32x4 acc[kRB][2][kPB];
 #pragma unroll
-    for (int i = 0; i < 2 + 2 * kPB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int pb = 0; pb < kPB; ++pb) acc[rb][h][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const Frag& f) {
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int pb = 0; pb < kPB; ++pb)
+            acc[rb][h][pb] = mfma16(as_bf16x8(f.a[rb]), as_bf16x8(f.b[h][pb]), acc[rb][h][pb]);
+    };
+    // the next half-step's LDS reads spread between this half-step's MFMAs
+    constexpr int kReads = kRB + 2 * kPB, kMfma = 2 * kRB * kPB;
+    constexpr int kEvery = kMfma / kReads;  // MFMAs after each read
+    static_assert(kEvery >= 1, "interleave");
+    auto interleave = [&]() {
+#pragma unroll
+      for (int i = 0; i < kReads; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kEvery, 0);
+      }
+      if constexpr (kMfma > kEvery * kReads)
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kEvery * kReads, 0);
+    };
+
+    Frag f0, f1;
+    barrier_lds_drained();  // step 0 landed
+    read_frag(f0, 0, 0);
+    int stage = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int next = stage == STAGES - 1 ? 0 : stage + 1;
+      read_frag(f1, stage, 1);
+      mma(f0);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      barrier_lds_drained();  // step kt + 1 landed; this wave's reads of step kt done
+      __builtin_amdgcn_sched_barrier(0);
+      read_frag(f0, next, 0);
+      mma(f1);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      stage = next;
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * kPB - (2 + 2 * kPB), 0);
-  };
 
-  Frag f0, f1;
-  barrier_lds_drained();  // row metadata stored; step 0 landed
-  read_frag(f0, 0, 0);
-  int stage = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int next = stage == kPcStages - 1 ? 0 : stage + 1;
-    read_frag(f1, stage, 1);
-    mma(f0);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    barrier_lds_drained();  // step kt + 1 landed; this wave's reads of step kt - 2 done
-    __builtin_amdgcn_sched_barrier(0);
-    read_frag(f0, next, 0);
-    mma(f1);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    stage = next;
-  }
-
-  // Epilogue: acc[rb][h][pb][i] is row 32 wm + 16 rb + 4 g4 + i, pair
-  // 96 nt + 32 wn + 16 pb + l16, low (h = 0) or high (h = 1) column.
+    // Stage the accumulators as fp32 rows in LDS: acc[rb][h][pb][i] is row
+    // BM/2 wm + 16 rb + 4 g4 + i, local pair BP/2 wn + 16 pb + l16, low (h = 0) or high.
+    barrier_lds_drained();  // every LDS read done, every producer load landed
+    float* ep = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int pb = 0; pb < kPB; ++pb) {
-    const int p = kPcBP * nt + kWP * wn + 16 * pb + l16;
-    const int mat = p / pairs_per_mat, rem = p - mat * pairs_per_mat;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 32 * wm + 16 * rb + 4 * g4 + i;
-        const int64_t dst = s_dst[mat == 0 ? 0 : 1][row];
-        if (dst < 0) continue;
-        store_pair(a, mat, dst, s_rope[row], rem >> 6, rem & 63, acc[rb][0][pb][i],
-                   acc[rb][1][pb][i]);
+        float* row = ep + ((BM / 2) * wm + 16 * rb + 4 * g4 + i) * kEpStride + kWP * wn + l16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int pb = 0; pb < kPB; ++pb) row[BP * h + 16 * pb] = acc[rb][h][pb][i];
       }
+    if (tid < BM) {
+      int64_t* meta = reinterpret_cast<int64_t*>(smem + Sh::kEpMetaOff);
+      meta[tid] = my_dq;
+      meta[BM + tid] = my_dkv;
+      meta[2 * BM + tid] = my_rope;
+    }
+    barrier_lds_drained();
   }
+
+  // Every thread rotates and stores groups of 8 pairs of one row (16-byte stores): all the
+  // LDS and sin/cos reads of its groups first, then the stores.
+  const float* ep = reinterpret_cast<const float*>(smem);
+  const int64_t* meta = reinterpret_cast<const int64_t*>(smem + Sh::kEpMetaOff);
+  constexpr int kGroups = BP / 8, kItems = BM * kGroups;
+  constexpr int kPer = (kItems + kThreads - 1) / kThreads;
+  EpGroup grp[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int it = min(tid + kThreads * j, kItems - 1);
+    const int row = it / kGroups, g = it - kGroups * row;
+    const int p0 = BP * nt + 8 * g;
+    const int mat = p0 / pairs_per_mat, rem = p0 - mat * pairs_per_mat;
+    const bool mine = kItems % kThreads == 0 || tid + kThreads * j < kItems;
+    grp[j].load(a, ep + row * kEpStride + 8 * g, BP, mat, rem,
+                mine ? meta[(mat == 0 ? 0 : BM) + row] : -1, meta[2 * BM + row]);
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) grp[j].store(a);
 }
 
 }  // namespace
@@ -488,9 +400,10 @@ __global__ __launch_bounds__(kPcThreads, 1) void qkv_pc_kernel(QkvArgs a) {
 namespace fdl {
 namespace {
 
-// Launch plan by row count (measured on MI355X at d_model 4096): up to 64 rows the
-// projection streams the weights (the narrow tiles give every CU work); above that the
-// producer/consumer kernel's wide tiles keep the MFMAs fed.
+// Launch plan by row count (measured on MI355X at d_model 4096): up to 128 rows the
+// projection streams the weights (32-pair tiles, 192 workgroups, 6-8 stages: 18.6 us at
+// 40 rows, 23 us at 128); above that the wide tiles keep the MFMAs fed (128 x 32-pair
+// tiles take 45 us at 192 rows against 36 us for the wide tiles).
 struct QkvPlan {
   void (*kernel)(QkvArgs);
   int bm;       // rows per tile
@@ -498,9 +411,17 @@ struct QkvPlan {
   int threads;  // per workgroup
 };
 
+constexpr int kPcBM = 128, kPcBP = 96;
+
+template <int BM, int BP, int NPROD, int STAGES>
+constexpr QkvPlan pc_plan() {
+  return {qkv_pc_kernel<BM, BP, NPROD, STAGES>, BM, BP, PcShape<BM, BP, NPROD, STAGES>::kThreads};
+}
+
 QkvPlan qkv_plan(int64_t n_rows) {
-  if (n_rows <= 64) return {qkv_stream_kernel<64, 32, 2>, 64, 32, kThreads};
-  return {qkv_pc_kernel, kPcBM, kPcBP, kPcThreads};
+  if (n_rows <= 64) return pc_plan<64, 32, 4, 8>();
+  if (n_rows <= 128) return pc_plan<128, 32, 4, 6>();
+  return pc_plan<kPcBM, kPcBP, 4, 4>();
 }
 
 // Compute units of the current device (cached per device).
@@ -521,7 +442,7 @@ int device_cus() {
 // Rows handed to the weight-streaming kernel at the end of a producer/consumer launch: a
 // remainder of at most 64 rows that would otherwise open one more round of workgroups on
 // the device (one workgroup per CU). At 576 rows: 4 full tiles (one round, 54 us) plus a
-// 64-row stream (22 us) instead of 5 tiles in two rounds (108 us).
+// 64-row stream (19 us) instead of 5 tiles in two rounds (~100 us).
 int64_t qkv_tail_rows(int64_t n_rows, int64_t n_pairs) {
   if (n_rows <= kPcBM) return 0;
   const int64_t tail = n_rows % kPcBM;
@@ -579,9 +500,9 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
               (long long)d_model, (long long)n_heads);
   FDL_REQUIRE(d_model <= (1 << 16), FDL_ERR_UNSUPPORTED,
               "fdl_qkv_rope_cache: d_model = %lld too large", (long long)d_model);
-  FDL_REQUIRE(d_model % (kKT * kStages) == 0, FDL_ERR_UNSUPPORTED,
+  FDL_REQUIRE(d_model % kDAlign == 0, FDL_ERR_UNSUPPORTED,
               "fdl_qkv_rope_cache: d_model = %lld is not a multiple of %d", (long long)d_model,
-              kKT * kStages);
+              kDAlign);
   FDL_REQUIRE(kv_packed == 0 || kv_packed == 1, FDL_ERR_SHAPE,
               "fdl_qkv_rope_cache: kv_packed must be 0 or 1");
   FDL_REQUIRE(!kv_packed || n_kv_rows == n_rows, FDL_ERR_SHAPE,
@@ -603,6 +524,11 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   FDL_REQUIRE_ALIGNED(wq, 16);
   FDL_REQUIRE_ALIGNED(wk, 16);
   FDL_REQUIRE_ALIGNED(wv, 16);
+  FDL_REQUIRE_ALIGNED(rope_sin, 16);
+  FDL_REQUIRE_ALIGNED(rope_cos, 16);
+  FDL_REQUIRE_ALIGNED(q_out, 16);
+  FDL_REQUIRE_ALIGNED(k_out, 16);
+  FDL_REQUIRE_ALIGNED(v_out, 16);
   FDL_REQUIRE((n_rows + 63) / 64 * (3 * n_heads * kHalf / 32) < (int64_t(1) << 31),
               FDL_ERR_UNSUPPORTED, "fdl_qkv_rope_cache: %lld rows is too many",
               (long long)n_rows);

@@ -78,7 +78,8 @@ int fdl_abi_version(void);
  *            overwritten with the rotated K / V of row r; kv_packed == 1 -> packed
  *            [n_rows][d_model] (n_kv_rows must equal n_rows).
  * Rows whose slot or rope_row is out of range are skipped by the kernel; use
- * fdl_validate_rows to reject them on the host.
+ * fdl_validate_rows to reject them on the host. x, the weights, the sin/cos tables and the
+ * outputs must be 16-byte aligned (d_model is a multiple of 256).
  */
 int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void* wv,
                        const float* rope_sin, const float* rope_cos, int64_t n_rope_rows,
