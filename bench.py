@@ -171,15 +171,83 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     t1.record()
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
-    # pass 2: per-kernel durations from events around every launch
+    # pass 2: per-kernel durations from events around every launch (these include the host's
+    # launch gaps where the host is slower than a short kernel)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
            for _ in range(steps)]
     for i in range(steps):
         step(evs[i])
     torch.cuda.synchronize()
-    per = {n: float(np.mean([evs[i][k].elapsed_time(evs[i][k + 1]) for i in range(steps)]) * 1e3)
-           for k, n in enumerate(names)}
-    return dict(Q=Q, total_ms=total_ms, per_kernel_us=per)
+    per_events = {n: float(np.mean([evs[i][k].elapsed_time(evs[i][k + 1]) for i in range(steps)]))
+                  * 1e3 for k, n in enumerate(names)}
+    # pass 3: per-kernel durations in the step's own sequence without host time: `steps` whole
+    # steps captured in a HIP graph and replayed (HIP events around the replays, on the stream
+    # the kernels run on); a kernel's duration is the step time minus that of the same graph
+    # without the kernel
+    ws = torch.empty(max(ops.attention_workspace_floats(plan, H), 4), dtype=torch.float32,
+                     device=dev)
+    kernels = {
+        "qkv_rope_cache": lambda: ops.qkv_rope_cache(d["x"], d["wq"], d["wk"], d["wv"], d["sin"],
+                                                     d["cos"], d["slot"], q, kc, vc, H),
+        "block_attention": lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
+                                                       lib.IMP_SOFTMAX_COLSUM, imp, workspace=ws),
+        "importance_accumulate_rank": lambda: ops.importance_rank(
+            scores, d["full_pos"], d["seg"], max_len, topk, TOPK, imp_part=imp, scale=1.0,
+            plan=plan, seg_keys=d["seg_keys"]),
+    }
+    def steps_of(names_in):
+        fns = [kernels[n] for n in names if n in names_in]
+        return lambda: [fn() for fn in fns]
+    graph_step = _graph_time(steps_of(names), steps)
+    per = {n: graph_step - _graph_time(steps_of([m for m in names if m != n]), steps)
+           for n in names}
+    # the graphs replay what the eager launches compute: one step eagerly and one step from a
+    # graph, from the same starting scores, bit for bit
+    scores.zero_()
+    for fn in kernels.values():
+        fn()
+    eager = [t.clone() for t in (q, att, topk, scores)]
+    g = _capture(lambda: [fn() for fn in kernels.values()], 1)
+    for _ in range(2):
+        scores.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        same = all(torch.equal(a, b) for a, b in zip(eager, (q, att, topk, scores)))
+        if not same:
+            break
+    return dict(Q=Q, total_ms=total_ms, per_kernel_us=per, per_kernel_events_us=per_events,
+                graph_matches_eager=same, graph_step_us=graph_step)
+
+
+def _capture(fn, reps: int):
+    """A HIP graph of `reps` calls of fn() (captured on a side stream after one warm call)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        fn()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(reps):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
+def _graph_time(fn, reps: int, replays: int = 3) -> float:
+    """Mean microseconds per call of fn() replayed from a graph of `reps` calls."""
+    import torch
+    g = _capture(fn, reps)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * replays)
 
 
 def run_torch_layer(reps: int = 20, seed: int = 2) -> dict:
@@ -846,6 +914,13 @@ def main() -> int:
                      "traffic": traffic.get("qkv_rope_cache"), "kernel": "qkv_rope_cache",
                      "traffic_source": TRAFFIC_FILE.name},
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
+        "kernel_timing": {"how": "--steps whole steps in a HIP graph replayed 3 times, HIP events "
+                                 "around the replays; a kernel's time = the step time minus that "
+                                 "of the same graph without the kernel",
+                          "graph_step_us": round(r["graph_step_us"], 3),
+                          "graph_matches_eager": r["graph_matches_eager"],
+                          "events_around_eager_launches_us": {
+                              k: round(v, 3) for k, v in r["per_kernel_events_us"].items()}},
     }
     if not args.no_torch:
         tl = run_torch_layer()
