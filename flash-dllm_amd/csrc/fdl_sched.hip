@@ -418,6 +418,166 @@ __global__ __launch_bounds__(kSchedThreads) void sched_pack_kernel(fdl_sched s) 
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Work list from the reference's block tables (fdl_work_from_blocks).
+//
+// Rows (batch, k_end, q0, q1) of the masked table, then of the tracked table
+// (generate.py:52-58, :146-163, :439-465), are grouped by (batch, k_end) in order of first
+// appearance; a group's rows are its masked rows (entry order) then its tracked rows, and
+// its masked rows are its importance rows. A group of up to 64 rows is one short tile, up
+// to 128 one mid tile, more one 256-row tile per 256 rows; tiles go to fixed-capacity
+// regions [long | mid | short] of the work array and unused items are zero (no rows, no
+// keys: the attention and importance kernels skip them). The same grouping and tile
+// classes as fdl.schedule.build_work, without the host: tiles stay in group order within a
+// class instead of longest first.
+constexpr int kWfbMaxEntries = 1024;
+constexpr int kWfbMaxSeq = 1024;
+
+struct WfbArgs {
+  const int64_t* masked;
+  const int64_t* tracked;
+  int32_t* work;
+  int32_t* row_idx;
+  int32_t* status;  // [4]: long, mid, short tiles, error flags (or NULL)
+  int n_masked, n_tracked, n_seq;
+  int64_t n_q_rows, max_k;
+  int cap_long, cap_mid, cap_short;
+};
+
+__global__ __launch_bounds__(kSchedThreads) void work_from_blocks_kernel(WfbArgs a) {
+  __shared__ int s_gid_of_b[kWfbMaxSeq];                      // first group of a batch row
+  __shared__ int s_gb[kWfbMaxEntries], s_gk[kWfbMaxEntries];  // group key (batch, k_end)
+  __shared__ int s_gm[kWfbMaxEntries], s_gt[kWfbMaxEntries];  // its masked / tracked rows
+  __shared__ int s_goff[kWfbMaxEntries], s_cur[kWfbMaxEntries];  // first row; a cursor
+  __shared__ int s_eg[kWfbMaxEntries], s_eoff[kWfbMaxEntries];   // entry: group, first row
+  __shared__ int4 s_e[kWfbMaxEntries];  // the entries (b, k_end, q0, q1); b = -1: dropped
+  __shared__ int s_used[3];
+  const int tid = threadIdx.x;
+  const int n = a.n_masked + a.n_tracked;
+  for (int i = tid; i < a.n_seq; i += kSchedThreads) s_gid_of_b[i] = -1;
+  // stage the tables (an entry outside the tables' ranges is dropped)
+  for (int i = tid; i < n; i += kSchedThreads) {
+    const int64_t* src = i < a.n_masked ? a.masked + 4 * int64_t(i)
+                                        : a.tracked + 4 * int64_t(i - a.n_masked);
+    const int64_t b = src[0], k = src[1], q0 = src[2], q1 = src[3];
+    const bool ok = b >= 0 && b < a.n_seq && k > 0 && k <= a.max_k && q0 >= 0 && q1 >= q0 &&
+                    q1 <= a.n_q_rows;
+    s_e[i] = ok ? make_int4(int(b), int(k), int(q0), int(q1)) : make_int4(-1, 0, 0, 0);
+  }
+  __syncthreads();
+  auto entry = [&](int i, int64_t (&e)[4]) {
+    const int4 v = s_e[i];
+    e[0] = v.x;
+    e[1] = v.y;
+    e[2] = v.z;
+    e[3] = v.w;
+  };
+  if (tid == 0) {
+    int err = 0, G = 0;
+    // groups in order of first appearance, with their masked and tracked row counts
+    for (int i = 0; i < n; ++i) {
+      int64_t e[4];
+      entry(i, e);
+      s_eg[i] = -1;
+      if (e[0] < 0) {
+        err |= 1;
+        continue;
+      }
+      const int b = int(e[0]), k = int(e[1]);
+      int g = s_gid_of_b[b];
+      if (g < 0 || s_gk[g] != k) {  // a new key, or a batch row under a second key count
+        int f = -1;
+        for (int j = 0; j < G && f < 0; ++j)
+          if (s_gb[j] == b && s_gk[j] == k) f = j;
+        if (f < 0) {
+          f = G++;
+          s_gb[f] = b;
+          s_gk[f] = k;
+          s_gm[f] = s_gt[f] = 0;
+          if (s_gid_of_b[b] < 0) s_gid_of_b[b] = f;
+        }
+        g = f;
+      }
+      s_eg[i] = g;
+      if (i < a.n_masked)
+        s_gm[g] += int(e[3] - e[2]);
+      else
+        s_gt[g] += int(e[3] - e[2]);
+    }
+    int off = 0;
+    for (int g = 0; g < G; ++g) {
+      s_goff[g] = off;
+      off += s_gm[g] + s_gt[g];
+    }
+    if (off > a.n_q_rows) err |= 2;
+    // first row of every entry: a group's masked entries in order, then its tracked ones
+    for (int kind = 0; kind < 2; ++kind) {
+      for (int g = 0; g < G; ++g) s_cur[g] = s_goff[g] + (kind ? s_gm[g] : 0);
+      for (int i = kind ? a.n_masked : 0; i < (kind ? n : a.n_masked); ++i) {
+        const int g = s_eg[i];
+        if (g < 0) continue;
+        int64_t e[4];
+        entry(i, e);
+        s_eoff[i] = s_cur[g];
+        s_cur[g] += int(e[3] - e[2]);
+      }
+    }
+    // tiles, in group order within each class
+    int nl = 0, nm = 0, ns = 0;
+    for (int g = 0; g < G; ++g) {
+      const int rows = s_gm[g] + s_gt[g], start = s_goff[g], n_imp = s_gm[g];
+      auto put = [&](int slot, int r0, int nr, int imp) {
+        u32x4* w = reinterpret_cast<u32x4*>(a.work + 8 * int64_t(slot));
+        w[0] = u32x4{uint32_t(s_gb[g]), 0u, uint32_t(s_gk[g]), uint32_t(r0)};
+        w[1] = u32x4{uint32_t(nr), uint32_t(imp), 0u, 0u};
+      };
+      if (rows == 0) continue;
+      if (rows <= 64) {
+        if (ns < a.cap_short) put(a.cap_long + a.cap_mid + ns, start, rows, n_imp);
+        else err |= 4;
+        ++ns;
+      } else if (rows <= 128) {
+        if (nm < a.cap_mid) put(a.cap_long + nm, start, rows, n_imp);
+        else err |= 4;
+        ++nm;
+      } else {
+        if (n_imp > 256) err |= 8;  // importance rows beyond one long tile are not counted
+        for (int t0 = 0; t0 < rows; t0 += 256) {
+          const int nr = min(256, rows - t0);
+          if (nl < a.cap_long) put(nl, start + t0, nr, t0 == 0 ? min(n_imp, nr) : 0);
+          else err |= 4;
+          ++nl;
+        }
+      }
+    }
+    s_used[0] = min(nl, a.cap_long);
+    s_used[1] = min(nm, a.cap_mid);
+    s_used[2] = min(ns, a.cap_short);
+    if (a.status) {
+      const u32x4 st = {uint32_t(nl), uint32_t(nm), uint32_t(ns), uint32_t(err)};
+      *reinterpret_cast<u32x4*>(a.status) = st;
+    }
+  }
+  __syncthreads();
+  // unused items of each region: zero (no rows, no keys)
+  const int cap[3] = {a.cap_long, a.cap_mid, a.cap_short};
+  for (int c = 0, base = 0; c < 3; base += cap[c], ++c)
+    for (int i = s_used[c] + tid; i < cap[c]; i += kSchedThreads) {
+      u32x4* w = reinterpret_cast<u32x4*>(a.work + 8 * int64_t(base + i));
+      w[0] = u32x4{0u, 0u, 0u, 0u};
+      w[1] = u32x4{0u, 0u, 0u, 0u};
+    }
+  // row lists: entry i's rows q0 .. q1 - 1 from its first row
+  for (int i = 0; i < n; ++i) {
+    if (s_eg[i] < 0) continue;
+    int64_t e[4];
+    entry(i, e);
+    const int rows = int(e[3] - e[2]), o = s_eoff[i];
+    for (int r = tid; r < rows; r += kSchedThreads)
+      if (o + r < a.n_q_rows) a.row_idx[o + r] = int32_t(e[2] + r);
+  }
+}
+
 int check_sched(const char* fn, const fdl_sched* s) {
   FDL_REQUIRE(s != nullptr, FDL_ERR_NULL, "%s: state is NULL", fn);
   FDL_REQUIRE(s->n_seq >= 1 && s->n_seq <= kMaxSeq, FDL_ERR_UNSUPPORTED,
@@ -472,6 +632,50 @@ extern "C" int fdl_sched_pack(const fdl_sched* state, void* stream) {
               (long long)state->work_cap);
   hipLaunchKernelGGL(sched_pack_kernel, dim3(1), dim3(kSchedThreads), 0,
                      static_cast<hipStream_t>(stream), *state);
+  FDL_HIP_CHECK(hipGetLastError());
+  return ok();
+}
+
+extern "C" int fdl_work_from_blocks(const int64_t* masked, int64_t n_masked, const int64_t* tracked,
+                                    int64_t n_tracked, int64_t n_seq, int64_t n_q_rows,
+                                    int64_t max_k, int32_t* work, int64_t cap_long,
+                                    int64_t cap_mid, int64_t cap_short, int32_t* row_idx,
+                                    int32_t* status, void* stream) {
+  using namespace fdl;
+  FDL_REQUIRE(n_masked >= 0 && n_tracked >= 0 && n_masked + n_tracked <= kWfbMaxEntries,
+              FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks: %lld table rows (at most %d)",
+              (long long)(n_masked + n_tracked), kWfbMaxEntries);
+  FDL_REQUIRE(n_seq >= 1 && n_seq <= kWfbMaxSeq, FDL_ERR_UNSUPPORTED,
+              "fdl_work_from_blocks: n_seq = %lld outside [1, %d]", (long long)n_seq, kWfbMaxSeq);
+  FDL_REQUIRE(n_q_rows >= 0 && n_q_rows < (int64_t(1) << 31) && max_k >= 1 &&
+                  max_k < (int64_t(1) << 31),
+              FDL_ERR_SHAPE, "fdl_work_from_blocks: n_q_rows / max_k out of range");
+  FDL_REQUIRE(cap_long >= 0 && cap_mid >= 0 && cap_short >= 0 &&
+                  cap_long + cap_mid + cap_short < (int64_t(1) << 30),
+              FDL_ERR_SHAPE, "fdl_work_from_blocks: capacities out of range");
+  FDL_REQUIRE((n_masked == 0 || masked) && (n_tracked == 0 || tracked), FDL_ERR_NULL,
+              "fdl_work_from_blocks: a table is NULL");
+  FDL_REQUIRE(work || cap_long + cap_mid + cap_short == 0, FDL_ERR_NULL,
+              "fdl_work_from_blocks: work is NULL");
+  FDL_REQUIRE(row_idx || n_q_rows == 0, FDL_ERR_NULL, "fdl_work_from_blocks: row_idx is NULL");
+  FDL_REQUIRE_ALIGNED(work, 16);
+  FDL_REQUIRE_ALIGNED(status, 16);
+  WfbArgs a;
+  a.masked = masked;
+  a.tracked = tracked;
+  a.work = work;
+  a.row_idx = row_idx;
+  a.status = status;
+  a.n_masked = int(n_masked);
+  a.n_tracked = int(n_tracked);
+  a.n_seq = int(n_seq);
+  a.n_q_rows = n_q_rows;
+  a.max_k = max_k;
+  a.cap_long = int(cap_long);
+  a.cap_mid = int(cap_mid);
+  a.cap_short = int(cap_short);
+  hipLaunchKernelGGL(work_from_blocks_kernel, dim3(1), dim3(kSchedThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
   FDL_HIP_CHECK(hipGetLastError());
   return ok();
 }

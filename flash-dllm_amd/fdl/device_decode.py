@@ -25,21 +25,9 @@ import torch
 
 from . import lib as _lib
 from . import ops
-from .schedule import AttnPlan, contiguous_page_table
+from .schedule import DEFAULT_PAGE_LOG2, AttnPlan, DeviceAttnPlan, contiguous_page_table
 
 I64, I32 = torch.int64, torch.int32
-
-
-class _DevicePlan(AttnPlan):
-    """An attention plan whose work items and row lists were built on the device."""
-
-    @property
-    def has_importance(self) -> bool:
-        return self._importance
-
-    @property
-    def n_work(self) -> int:
-        return self._n_work
 
 
 class DeviceScheduler:
@@ -109,14 +97,9 @@ class DeviceScheduler:
         n_long, n_mid, n_short = (int(summ[_lib.SUM_N_LONG]), int(summ[_lib.SUM_N_MID]),
                                   int(summ[_lib.SUM_N_SHORT]))
         q = int(summ[_lib.SUM_Q])
-        p = _DevicePlan(work=np.zeros((0, 8), np.int32), row_idx=np.zeros(max(q, 1), np.int32),
-                        page_table=self.page_table, page_log2=5, n_long=n_long, n_mid=n_mid)
-        p._n_work = n_long + n_mid + n_short
-        p._importance = importance
-        p.work_d = self.work
-        p.row_idx_d = self.row_idx
-        p.page_table_d = self.page_table_d
-        return p
+        return DeviceAttnPlan(self.work, self.row_idx, q, self.page_table, self.page_table_d,
+                              DEFAULT_PAGE_LOG2, n_long, n_mid, n_long + n_mid + n_short,
+                              importance)
 
 
 @torch.no_grad()

@@ -122,6 +122,8 @@ SIGNATURES: dict[str, tuple] = {
     "fdl_sched_pass1": (ctypes.c_int, [_p, _p, _p, _p]),
     "fdl_sched_verify_accept": (ctypes.c_int, [_p, _p, _p]),
     "fdl_sched_pack": (ctypes.c_int, [_p, _p]),
+    "fdl_work_from_blocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64,
+                                            _i64, _i64, _p, _p, _p]),
     "fdl_validate_rows": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32]),
     "fdl_validate_work": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i64]),
     "fdl_validate_vblocks": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i64, _i32]),

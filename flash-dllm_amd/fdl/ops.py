@@ -7,10 +7,11 @@ a GPU is an error.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import lib as _lib
-from .schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, MID_TILE_ROWS, AttnPlan
+from .schedule import LONG_TILE_ROWS, MAX_TILE_ROWS, MID_TILE_ROWS, AttnPlan, DeviceAttnPlan
 
 BF16 = torch.bfloat16
 
@@ -134,7 +135,8 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     d_model = q.shape[1]
     stream = _stream(q)
     n_row_idx = max(int(plan.row_idx.size), 1)
-    if imp_mode == _lib.IMP_SOFTMAX_COLSUM and plan.n_long and int(plan.work[:plan.n_long, 5].max()) > MID_TILE_ROWS:
+    if (imp_mode == _lib.IMP_SOFTMAX_COLSUM and plan.n_long and plan.work.shape[0] >= plan.n_long
+            and int(plan.work[:plan.n_long, 5].max()) > MID_TILE_ROWS):
         raise _lib.FdlError(_lib.FDL_ERR_UNSUPPORTED,
                             f"softmax-colsum importance needs at most {MID_TILE_ROWS} importance rows per sequence")
     if imp_mode == _lib.IMP_SOFTMAX_COLSUM and workspace is None:
@@ -153,6 +155,38 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                   n_row_idx, tile_rows, float(softmax_scale), out.data_ptr(), int(imp_mode),
                   _ptr(imp_part), _ptr(workspace), 0 if workspace is None else workspace.numel(),
                   stream)
+
+
+def work_from_blocks(masked: torch.Tensor, tracked: torch.Tensor, n_seq: int, n_q_rows: int,
+                     page_table: np.ndarray, page_table_d: torch.Tensor, page_log2: int,
+                     status: torch.Tensor | None = None) -> DeviceAttnPlan:
+    """An attention plan built on the device from the reference's block tables (int64
+    [n, 4] device tensors, rows (batch, k_end, q0, q1); fdl_work_from_blocks): no host
+    copy of the tables. Regions: n_q_rows // 128 long, n_seq mid and n_seq short items."""
+    dev = page_table_d.device
+    tabs = []
+    for name, t in (("masked", masked), ("tracked", tracked)):
+        if t is None or t.numel() == 0:
+            tabs.append(None)
+            continue
+        _need(t, name, torch.int64, 2, dev)
+        if t.shape[1] != 4:
+            raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} must be [n, 4]")
+        tabs.append(t.contiguous())
+    n_m = 0 if tabs[0] is None else tabs[0].shape[0]
+    n_t = 0 if tabs[1] is None else tabs[1].shape[0]
+    # every 256-row tile belongs to a group of more than 128 rows: at most n_q_rows // 128
+    cap_long, cap_mid, cap_short = n_q_rows // MID_TILE_ROWS, n_seq, n_seq
+    work = torch.empty((max(cap_long + cap_mid + cap_short, 1), 8), dtype=torch.int32, device=dev)
+    row_idx = torch.empty(max(n_q_rows, 1), dtype=torch.int32, device=dev)
+    if status is not None:
+        _need(status, "status", torch.int32, 1, dev)
+    max_k = int(page_table.shape[1]) << page_log2
+    _lib.call("fdl_work_from_blocks", _ptr(tabs[0]), n_m, _ptr(tabs[1]), n_t, n_seq, n_q_rows,
+              max_k, work.data_ptr(), cap_long, cap_mid, cap_short, row_idx.data_ptr(),
+              _ptr(status), _stream(page_table_d))
+    return DeviceAttnPlan(work, row_idx, n_q_rows, page_table, page_table_d, page_log2, cap_long,
+                          cap_mid, cap_long + cap_mid + cap_short, n_m > 0)
 
 
 def importance_accumulate(imp_part: torch.Tensor, plan: AttnPlan, scale: float,

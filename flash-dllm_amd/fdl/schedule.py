@@ -232,6 +232,30 @@ class AttnPlan:
                   n_q_rows, p.ctypes.data, p.shape[0], p.shape[1], self.page_log2, n_slots)
 
 
+class DeviceAttnPlan(AttnPlan):
+    """An attention plan whose work items and row list were built on the device
+    (fdl_sched_pack or fdl_work_from_blocks): the host knows only the class regions of the
+    work array (their items past the built ones are empty) and the number of rows."""
+
+    def __init__(self, work_d, row_idx_d, n_rows: int, page_table: np.ndarray, page_table_d,
+                 page_log2: int, n_long: int, n_mid: int, n_work: int, importance: bool):
+        super().__init__(work=np.zeros((0, 8), np.int32), row_idx=np.zeros(max(n_rows, 1), np.int32),
+                         page_table=page_table, page_log2=page_log2, n_long=n_long, n_mid=n_mid)
+        self._n_work = n_work
+        self._importance = importance
+        self.work_d = work_d
+        self.row_idx_d = row_idx_d
+        self.page_table_d = page_table_d
+
+    @property
+    def has_importance(self) -> bool:
+        return self._importance
+
+    @property
+    def n_work(self) -> int:
+        return self._n_work
+
+
 def make_plan(seqs: list[SeqRows], page_table: np.ndarray, page_log2: int = DEFAULT_PAGE_LOG2,
               device=None, max_rows: int = MAX_TILE_ROWS) -> AttnPlan:
     work, row_idx, n_long, n_mid = build_work(seqs, max_rows)

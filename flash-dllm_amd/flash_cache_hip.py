@@ -38,7 +38,8 @@ Where the results differ from the reference's (same arithmetic, different roundi
 
 `info` (unused by the reference kernels) may carry a precomputed fdl.schedule.AttnPlan;
 otherwise the plan is derived from the masked/tracked block tables once per forward
-(the same table objects are passed to every layer) and reused by all layers. A plan over a
+(the same table objects are passed to every layer) and reused by all layers: on the GPU
+(fdl_work_from_blocks, no host copy) when the tables are GPU tensors. A plan over a
 paged K/V pool carries `kv_slot`, the cache slots of the query rows; query_pos_flat then
 indexes only the RoPE tables, and key_pos_flat (verify) and attn_scores use pool slots.
 """
@@ -53,7 +54,8 @@ import torch.nn.functional as F
 
 from fdl import lib as _lib
 from fdl import ops
-from fdl.schedule import AttnPlan, contiguous_page_table, make_plan, seqs_from_reference_blocks
+from fdl.schedule import (DEFAULT_PAGE_LOG2, AttnPlan, contiguous_page_table, make_plan,
+                          seqs_from_reference_blocks)
 
 _plan_cache: dict = {}
 _workspace: dict = {}
@@ -65,14 +67,37 @@ def _as_np_table(t) -> np.ndarray:
     return t.detach().to("cpu").numpy().astype(np.int64).reshape(-1, 4)
 
 
-def _plan_from_tables(masked, tracked, n_seq: int, max_length: int, device) -> AttnPlan:
-    """AttnPlan for the reference's block tables, cached on the identity of the tables."""
-    key = (id(masked), id(tracked), n_seq, max_length, str(device))
+def _on_device(t, device) -> bool:
+    return isinstance(t, torch.Tensor) and t.device == torch.device(device)
+
+
+def _plan_from_tables(masked, tracked, n_seq: int, max_length: int, n_rows: int,
+                      device) -> AttnPlan:
+    """AttnPlan for the reference's block tables, cached on the identity of the tables (every
+    layer of a forward gets the same table objects). Tables on the GPU are turned into the
+    work list there (fdl_work_from_blocks: no host copy, no synchronisation); host tables
+    through fdl.schedule."""
+    key = (id(masked), id(tracked), n_seq, max_length, n_rows, str(device))
     hit = _plan_cache.get("entry")
     if hit is not None and hit[0] == key and hit[1]() is masked and hit[2]() is tracked:
         return hit[3]
-    seqs = seqs_from_reference_blocks(_as_np_table(masked), _as_np_table(tracked), importance=True)
-    plan = make_plan(seqs, contiguous_page_table(n_seq, max_length), device=device)
+    empty = lambda t: t is None or (isinstance(t, (list, tuple)) and len(t) == 0)  # noqa: E731
+    on_dev = all(empty(t) or _on_device(t, device) for t in (masked, tracked)) and not (
+        empty(masked) and empty(tracked))
+    table = contiguous_page_table(n_seq, max_length)
+    if on_dev:
+        key_t = ("page_table", n_seq, max_length, str(device))
+        table_d = _plan_cache.get(key_t)
+        if table_d is None:
+            table_d = torch.from_numpy(table).to(device)
+            _plan_cache[key_t] = table_d
+        as_i64 = lambda t: None if empty(t) else t.reshape(-1, 4).to(torch.int64)  # noqa: E731
+        plan = ops.work_from_blocks(as_i64(masked), as_i64(tracked), n_seq, n_rows, table,
+                                    table_d, DEFAULT_PAGE_LOG2)
+    else:
+        seqs = seqs_from_reference_blocks(_as_np_table(masked), _as_np_table(tracked),
+                                          importance=True)
+        plan = make_plan(seqs, table, device=device)
     ref = lambda t: weakref.ref(t) if isinstance(t, torch.Tensor) else (lambda: t)  # noqa: E731
     _plan_cache["entry"] = (key, ref(masked), ref(tracked), plan)
     return plan
@@ -244,7 +269,8 @@ def flash_fused_elastic_cache(self, x: torch.Tensor, block_idx, positions, lengt
         n_rows = x.shape[0]
         if n_rows > 0:
             plan = info if isinstance(info, AttnPlan) else _plan_from_tables(
-                query_masked_blocks, query_tracked_blocks, batch_size, max_length, x.device)
+                query_masked_blocks, query_tracked_blocks, batch_size, max_length, n_rows,
+                x.device)
             if plan.kv_slot is not None:
                 # paged pool: positions pick the RoPE rows, the plan's slots the cache rows
                 ops.qkv_rope_cache(x_normed, self.q_proj.weight, self.k_proj.weight,

@@ -381,6 +381,32 @@ int fdl_sched_verify_accept(const fdl_sched* state, const double* prob, void* st
  * work items; the summary. Replaces generate.py:364-383 (after the ranking) and :439-467. */
 int fdl_sched_pack(const fdl_sched* state, void* stream);
 
+/*
+ * Attention work list from the reference's block tables, on the device: no host copy of
+ * the tables. The reference's attention launches consume its masked and tracked block
+ * tables (rows (batch, k_end, q0, q1), generate.py:52-58, :146-163, :439-465; launched at
+ * flash_cache_triton.py:561-607); this builds the work items and row list that
+ * fdl_block_attention takes from them.
+ *   masked, tracked int64 [n][4] (device), n_masked + n_tracked <= 1024
+ *   rows of a (batch, k_end) pair are grouped in order of first appearance: its masked rows
+ *   (the importance rows) then its tracked rows; at most n_seq such pairs (the reference
+ *   has one k_end per batch row). A group of up to 64 rows is one 64-row tile, up to 128 one
+ *   128-row tile, more one 256-row tile per 256 rows.
+ *   work int32 [cap_long + cap_mid + cap_short][8], 16-byte aligned: the 256-row tiles from
+ *   item 0, the 128-row tiles from item cap_long, the 64-row tiles from cap_long + cap_mid;
+ *   unused items are zero (no rows, no keys), which fdl_block_attention and
+ *   fdl_importance_accumulate skip, so each region can be launched whole. cap_long =
+ *   n_q_rows / 128 and cap_mid = cap_short = n_seq always suffice.
+ *   row_idx int32 [n_q_rows]; status int32 [4] (16-byte aligned) or NULL: tiles of each
+ *   class and error flags (1: an entry out of range, dropped; 2: more rows than n_q_rows;
+ *   4: a region over capacity; 8: more than 256 importance rows in a group).
+ * One workgroup; enqueued on `stream`.
+ */
+int fdl_work_from_blocks(const int64_t* masked, int64_t n_masked, const int64_t* tracked,
+                         int64_t n_tracked, int64_t n_seq, int64_t n_q_rows, int64_t max_k,
+                         int32_t* work, int64_t cap_long, int64_t cap_mid, int64_t cap_short,
+                         int32_t* row_idx, int32_t* status, void* stream);
+
 /* every slot in [0, n_kv_rows), every rope_row (or slot when rope_row is NULL) in
  * [0, n_rope_rows), and no slot repeated (two rows writing one cache row race). */
 int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, int64_t n_rows,

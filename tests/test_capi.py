@@ -106,6 +106,13 @@ def test_launchers_reject_bad_scalars_without_gpu():
         setattr(st, name, 8)
     st.q_cap = -1
     _expect(lib.FDL_ERR_SHAPE, "fdl_sched_pack", ctypes.byref(st), None)
+    # device work list from block tables: too many entries, no sequences, NULL tables
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks", None, 1000, None, 25, 8, 64, 1024,
+            None, 0, 8, 8, None, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks", None, 1, None, 1, 0, 64, 1024, None,
+            0, 8, 8, None, None, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_work_from_blocks", None, 1, None, 1, 8, 64, 1024, None, 0, 8,
+            8, None, None, None)
     # every other entry point: an empty call returns before any pointer is read
     lib.call("fdl_importance_rank", None, 10, None, 10, None, 0, 16, None, 0, None)
     lib.call("fdl_importance_accumulate_rank", None, 32, 1.0, None, 1, 4, 5, None, None, 10,
