@@ -1074,16 +1074,22 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_ptr)smem));
   const int pc = lane & 15;
   // wave w loads keys 8 w .. 8 w + 7 of block blk: load i covers keys 8 w + 4 i + lane / 16
-  // (1 KB of K, 1 KB of V), LDS chunk lane % 16 of each key row. When those 8 keys share a
-  // page (k_begin % 8 == 0) their slots come from one scalar page-table load; keys past
-  // k_end repeat the last key.
+  // (1 KB of K, 1 KB of V), LDS chunk lane % 16 of each key row; keys past k_end repeat the
+  // last key. The slots come from the staged slot map: a page-table read here is a vector
+  // load, and the wait for it would also wait for every block load in flight (the ring's
+  // look-ahead). Without a staged map, when the 8 keys share a page (k_begin % 8 == 0) their
+  // slots come from one page-table entry.
   const bool scalar_pages = (k_begin & 7) == 0 && pl >= 3;
   const int64_t slot_last = n_blk > 0 ? lookup(k_end - 1) : 0;
   auto issue = [&](int blk) {
     const uint32_t st_lds = smem_lds + uint32_t((blk % kLongStages) * kStageBytes);
     const int n0 = k_begin + kTileN * blk;
     int64_t slots[2];
-    if (scalar_pages) {
+    if (slots_staged) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        slots[i] = slot_buf[min(n0 + 8 * wave + 4 * i + (lane >> 4), k_end - 1) - k_begin];
+    } else if (scalar_pages) {
       const int nf = __builtin_amdgcn_readfirstlane(n0 + 8 * wave);
       const int64_t base = nf < k_end ? int64_t(ptab[nf >> pl]) << pl : 0;
 #pragma unroll
