@@ -32,6 +32,7 @@
 #include "fdl_device.h"
 #include "fdl_host.h"
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -373,8 +374,9 @@ __device__ __forceinline__ bool verify_visible(int T, int S, int r, int j) {
 //   [n_blk, 2 n_blk)    softmax importance without the LDS store: the cache blocks again,
 //                       K only, last block first
 //   n_blk               verify only (when the block has rows): the in-block keys
-template <int RB, int NC, bool kVerify>
+template <int RB, int NC, bool kVerify, int HPW = 1>
 __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
+  static_assert(HPW == 1 || (kVerify && HPW == 2), "several heads per workgroup: verify only");
   constexpr int kRows = 16 * RB * NC;
   constexpr int kSt = kStages;  // LDS ring depth
   __shared__ __align__(1024) uint8_t smem[kSt * kStageBytes];
@@ -391,12 +393,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
 
   const int tid = threadIdx.x;
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
-  // wavefront executes only its own role's barriers (both roles execute 2 + n_steps).
+  // wavefront executes only its own role's barriers (both roles execute 2 + HPW n_steps).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const bool producer = wave >= NC;
   const int wr = producer ? wave - NC : wave;  // producer index or consumer index
   const int l16 = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y;
+  // heads h .. h + HPW - 1, one after the other: the key steps of every head run through
+  // the same LDS ring, so the next head's first blocks load while this head finishes
+  const int h = blockIdx.y * HPW;
   const int64_t D = a.d_model;
   const int col0 = h * kHeadDim;
 
@@ -461,10 +465,13 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   auto block_of = [&](int step) {
     return two_pass && step >= n_blk ? 2 * n_blk - 1 - step : step;
   };
-  auto stage_of = [&](int step) { return block_of(step) % kSt; };
-  // DMA per producer for step `step` (0: past the end, or a block still resident)
+  // Global step S = n_steps j + s: step s of head j. With several heads (verify: every step
+  // a fresh block) step S lives in stage S % kSt.
+  const int n_all = HPW * n_steps;
+  auto stage_of = [&](int step) { return (HPW > 1 ? step : block_of(step)) % kSt; };
+  // DMA per producer for global step `step` (0: past the end, or a block still resident)
   auto loads = [&](int step) {
-    if (step >= n_steps) return 0;
+    if (step >= n_all) return 0;
     if (!kVerify && step >= n_blk) return step - n_blk < kSt ? 0 : kDmaPerTile;
     return 2 * kDmaPerTile;
   };
@@ -505,9 +512,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     // Load i of producer wr fills LDS bytes [1024 q, 1024 q + 1024) of a tile, q = 4 wr + i:
     // keys 4q .. 4q + 3; lane -> key 4q + lane / 16, LDS chunk lane % 16.
     const int pc = lane & 15;
-    auto issue = [&](int s) {
-      if (loads(s) == 0) return;
-      uint8_t* st = smem + stage_of(s) * kStageBytes;
+    auto issue = [&](int gs) {
+      if (loads(gs) == 0) return;
+      uint8_t* st = smem + stage_of(gs) * kStageBytes;
+      const int hj = HPW > 1 ? gs / n_steps : 0;  // head of the step
+      const int s = gs - hj * n_steps;            // its step within the head
+      const int colh = col0 + hj * kHeadDim;
       const bool in_blk = kVerify && s >= n_blk;
       const bool k_only = !kVerify && s >= n_blk;
       const int n0 = k_begin + kTileN * block_of(s);
@@ -519,12 +529,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         if (in_blk) {
           // in-block key 64 (s - n_blk) + key: query row blk_row0 + that (checked above)
           const int64_t r = int64_t(blk_row0) + min(kTileN * (s - n_blk) + key, n_in - 1);
-          ks = a.kblk + r * D + col0;
-          vs = a.vblk + r * D + col0;
+          ks = a.kblk + r * D + colh;
+          vs = a.vblk + r * D + colh;
         } else {
           const int64_t slot = slot_of(min(n0 + key, k_end - 1));
-          ks = a.k + slot * D + col0;
-          vs = a.v + slot * D + col0;
+          ks = a.k + slot * D + colh;
+          vs = a.v + slot * D + colh;
         }
         const int kc = pc ^ (key & 15), vc = pc ^ ((key & 7) << 1);
         __builtin_amdgcn_global_load_lds((glb_ptr)(ks + 8 * kc), (lds_ptr)(st + 1024 * q), 16,
@@ -539,7 +549,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       wait_vmcnt(later_loads(0, kSt - 1));  // step 0 landed (steps 0 .. kSt - 1 issued)
     }
     barrier_only();  // #1
-    for (int s = 0; s < n_steps; ++s) {
+    for (int s = 0; s < n_all; ++s) {
       wait_vmcnt(later_loads(s + 1, s + kSt - 1));  // step s + 1 landed
       barrier_only();  // consumers are done with step s
       // step s + kSt lives in the stage of step s (a resident block's stage is kept)
@@ -562,21 +572,25 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       const int64_t q = kVerify ? int64_t(row0) + r : int64_t(a.row_idx[roff + r]);
       if (q >= 0 && q < a.n_q_rows) qrow[rb] = q;
     }
-#pragma unroll
-    for (int sd = 0; sd < 4; ++sd) {
-      u32x4 v = {0, 0, 0, 0};
-      if (qrow[rb] >= 0) v = ld16(a.q + qrow[rb] * D + col0 + 32 * sd + 8 * g);
-      qf[rb][sd] = as_bf16x8(v);
-    }
   }
+  // the rows' Q columns of the head at column colh, and a fresh softmax state
   RowState<RB> st;
+  auto begin_head = [&](int colh) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    st.m[rb] = -INFINITY;
-    st.l[rb] = 0.f;
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-    for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+      for (int sd = 0; sd < 4; ++sd) {
+        u32x4 v = {0, 0, 0, 0};
+        if (qrow[rb] >= 0) v = ld16(a.q + qrow[rb] * D + colh + 32 * sd + 8 * g);
+        qf[rb][sd] = as_bf16x8(v);
+      }
+      st.m[rb] = -INFINITY;
+      st.l[rb] = 0.f;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  begin_head(col0);
   const bool wave_imp = 16 * RB * wr < n_imp;
   const int imp_waves = (n_imp + 16 * RB - 1) / (16 * RB);
   float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
@@ -596,12 +610,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       }
     }
   };
-  auto write_out = [&]() {
+  auto write_out = [&](int colh) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       if (qrow[rb] < 0) continue;
       const float inv = st.l[rb] > 0.f ? 1.f / st.l[rb] : 0.f;
-      uint16_t* orow = a.out + qrow[rb] * D + col0;
+      uint16_t* orow = a.out + qrow[rb] * D + colh;
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         const f32x4 o = st.o[rb][db];
@@ -646,110 +660,113 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   }
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
-  for (int s = 0; s < n_steps; ++s) {
-    const int stage = stage_of(s);
-    const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
-    const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
-    const bool pass2 = !kVerify && s >= n_blk;
-    const bool in_blk = kVerify && inblock && s >= n_blk;
-    const int n0 = k_begin + kTileN * block_of(s);
-    if (two_pass && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
-    if (in_blk) {
-      const int br = a.block_rows;
-      const int j0 = kTileN * (s - n_blk);  // first in-block key of the step
-      int vT = 0, vS = 0;
-      if (a.vmeta) {
-        vT = a.vmeta[2 * vb_idx];
-        vS = a.vmeta[2 * vb_idx + 1];
-      }
-      attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
-        const int r = 16 * (wr * RB + rb) + l16;  // row of this workgroup
-        const int rr = r + kRows * half_v;          // row of the block
-        const int j = j0 + 16 * kb + 4 * g + ii;
-        if (j >= n_in || r >= n_rows) return -INFINITY;
-        const bool vis = a.vmeta ? verify_visible(vT, vS, rr, j)
-                                 : a.mask[(int64_t(vb_idx) * br + rr) * br + j] != 0;
-        return vis ? 0.f : -INFINITY;
-      }, [](int, const f32x4 (&)[4], float) {});
-    } else if (!pass2) {
-      // keys past k_end (the tail of the last block) get a -infinity bias
-      const int n_left = k_end - n0;
-      float kbias[4][4];
+  for (int hj = 0; hj < HPW; ++hj) {
+    if (hj > 0) begin_head(col0 + hj * kHeadDim);
+    for (int s = 0; s < n_steps; ++s) {
+      const int stage = stage_of(hj * n_steps + s);
+      const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
+      const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
+      const bool pass2 = !kVerify && s >= n_blk;
+      const bool in_blk = kVerify && inblock && s >= n_blk;
+      const int n0 = k_begin + kTileN * block_of(s);
+      if (two_pass && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
+      if (in_blk) {
+        const int br = a.block_rows;
+        const int j0 = kTileN * (s - n_blk);  // first in-block key of the step
+        int vT = 0, vS = 0;
+        if (a.vmeta) {
+          vT = a.vmeta[2 * vb_idx];
+          vS = a.vmeta[2 * vb_idx + 1];
+        }
+        attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
+          const int r = 16 * (wr * RB + rb) + l16;  // row of this workgroup
+          const int rr = r + kRows * half_v;          // row of the block
+          const int j = j0 + 16 * kb + 4 * g + ii;
+          if (j >= n_in || r >= n_rows) return -INFINITY;
+          const bool vis = a.vmeta ? verify_visible(vT, vS, rr, j)
+                                   : a.mask[(int64_t(vb_idx) * br + rr) * br + j] != 0;
+          return vis ? 0.f : -INFINITY;
+        }, [](int, const f32x4 (&)[4], float) {});
+      } else if (!pass2) {
+        // keys past k_end (the tail of the last block) get a -infinity bias
+        const int n_left = k_end - n0;
+        float kbias[4][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          kbias[kb][ii] = 16 * kb + 4 * g + ii < n_left ? 0.f : -INFINITY;
-      const int blk = block_of(s);
-      attend_block<RB>(
-          st, qf, kt, vt, a.scale_log2, [&](int, int kb, int ii) { return kbias[kb][ii]; },
-          [&](int rb, const f32x4 (&p)[4], float m_use) {
-            const int r = 16 * (wr * RB + rb) + l16;
-            if (store && r < kStoreRows) {
-              // row r, keys 16 kb + 4 g .. + 3 of block blk; then the row's maximum
-              float* rec = ws_tile + int64_t(blk) * kWsBlock;
+          for (int ii = 0; ii < 4; ++ii)
+            kbias[kb][ii] = 16 * kb + 4 * g + ii < n_left ? 0.f : -INFINITY;
+        const int blk = block_of(s);
+        attend_block<RB>(
+            st, qf, kt, vt, a.scale_log2, [&](int, int kb, int ii) { return kbias[kb][ii]; },
+            [&](int rb, const f32x4 (&p)[4], float m_use) {
+              const int r = 16 * (wr * RB + rb) + l16;
+              if (store && r < kStoreRows) {
+                // row r, keys 16 kb + 4 g .. + 3 of block blk; then the row's maximum
+                float* rec = ws_tile + int64_t(blk) * kWsBlock;
 #pragma unroll
-              for (int kb = 0; kb < 4; ++kb)
-                *reinterpret_cast<f32x4*>(rec + r * kTileN + 16 * kb + 4 * g) = p[kb];
-              if (g == 0) rec[kStoreRows * kTileN + r] = m_use;
+                for (int kb = 0; kb < 4; ++kb)
+                  *reinterpret_cast<f32x4*>(rec + r * kTileN + 16 * kb + 4 * g) = p[kb];
+                if (g == 0) rec[kStoreRows * kTileN + r] = m_use;
+              }
+            });
+        if (imp_raw && wr < 4) {
+          // consumer wr < 4: the 16 keys of key block kb = wr
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sd = 0; sd < 4; ++sd)
+            acc = mfma16(as_bf16x8(qsum_frag_buf[sd][lane]), k_frag(kt, wr, sd, l16, g), acc);
+          const int n = n0 + 16 * wr + l16;
+          if (g == 0 && n < k_end) {
+            const float v = qsum_dot(acc);
+            if constexpr (!kVerify) {
+              if (slots_staged) raw_buf[n - k_begin] = v;
+              else imp_out[slot_of(n)] = v;
             }
-          });
-      if (imp_raw && wr < 4) {
-        // consumer wr < 4: the 16 keys of key block kb = wr
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          }
+        }
+        if (imp_soft && s == n_blk - 1) {
+          // end of the first pass: the rows' log2-sum-exp for the second pass
 #pragma unroll
-        for (int sd = 0; sd < 4; ++sd)
-          acc = mfma16(as_bf16x8(qsum_frag_buf[sd][lane]), k_frag(kt, wr, sd, l16, g), acc);
-        const int n = n0 + 16 * wr + l16;
-        if (g == 0 && n < k_end) {
-          const float v = qsum_dot(acc);
-          if constexpr (!kVerify) {
-            if (slots_staged) raw_buf[n - k_begin] = v;
-            else imp_out[slot_of(n)] = v;
+          for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+          l_reduced = true;
+          if (g == 0) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              lse_buf[16 * (wr * RB + rb) + l16] =
+                  st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
+          }
+        }
+      } else {
+        if (s == n_blk) {
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
+        }
+        if (wave_imp) {
+          float cs[4];
+          column_sums<RB>(cs, qf, kt, [&](int rb, int ii, float sv) {
+            return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
+                       ? fast_exp2(sv * a.scale_log2 - lse_r[rb][ii])
+                       : 0.f;
+          });
+          if (g == 0) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) imp_buf[s & 1][wr][16 * kb + l16] = cs[kb];
           }
         }
       }
-      if (imp_soft && s == n_blk - 1) {
-        // end of the first pass: the rows' log2-sum-exp for the second pass
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
-        l_reduced = true;
-        if (g == 0) {
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-            lse_buf[16 * (wr * RB + rb) + l16] =
-                st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
-        }
-      }
-    } else {
-      if (s == n_blk) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) lse_r[rb][ii] = lse_buf[16 * (wr * RB + rb) + 4 * g + ii];
-      }
-      if (wave_imp) {
-        float cs[4];
-        column_sums<RB>(cs, qf, kt, [&](int rb, int ii, float sv) {
-          return 16 * (wr * RB + rb) + 4 * g + ii < n_imp
-                     ? fast_exp2(sv * a.scale_log2 - lse_r[rb][ii])
-                     : 0.f;
-        });
-        if (g == 0) {
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) imp_buf[s & 1][wr][16 * kb + l16] = cs[kb];
-        }
-      }
+      barrier_lds_drained();  // step s consumed; step s + 1 landed
     }
-    barrier_lds_drained();  // step s consumed; step s + 1 landed
-  }
-  if (two_pass && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
-  // the output first: its accumulators are then free for the importance epilogue
-  if (!l_reduced) {
+    if (two_pass && n_steps > 0) flush_imp(n_steps - 1, k_begin + kTileN * block_of(n_steps - 1));
+    // the output first: its accumulators are then free for the importance epilogue
+    if (!l_reduced) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+      for (int rb = 0; rb < RB; ++rb) st.l[rb] = xsum(st.l[rb]);
+    }
+    write_out(col0 + hj * kHeadDim);
   }
-  write_out();
   if constexpr (!kVerify) {
     if (imp_raw && slots_staged) {
       // the last step's barrier made every block's sums visible
@@ -1295,6 +1312,36 @@ hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, h
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int attn_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Flash-Verify launch: one workgroup per (block tile, head), one per CU at a time. A grid
+// that would take more than one round of workgroups runs two heads per workgroup instead,
+// so the second head's blocks stream in behind the first head's instead of paying a second
+// round's start-up.
+template <int RB, int NC>
+hipError_t launch_verify(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
+  if (n_heads % 2 == 0 && n_tiles * n_heads > attn_device_cus()) {
+    hipLaunchKernelGGL((attn_kernel<RB, NC, true, 2>),
+                       dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads / 2)),
+                       dim3(64 * (NC + kProducers)), 0, s, args);
+    return hipGetLastError();
+  }
+  return launch_attn<RB, NC, true>(args, n_tiles, n_heads, s);
+}
+
 }  // namespace
 }  // namespace fdl
 
@@ -1579,12 +1626,12 @@ extern "C" int fdl_verify_attention(const void* q, const void* k_blk, const void
   // workgroups per block (each attends to every in-block key)
   hipError_t e;
   if (block_rows <= 64) {
-    e = launch_attn<1, 4, true>(args, n_vblocks, n_heads, s);
+    e = launch_verify<1, 4>(args, n_vblocks, n_heads, s);
   } else {
     FDL_REQUIRE(n_vblocks < (int64_t(1) << 30), FDL_ERR_SHAPE,
                 "fdl_verify_attention: n_vblocks out of range");
     args.split = block_rows > 128 ? 1 : 0;
-    e = launch_attn<1, 8, true>(args, block_rows > 128 ? 2 * n_vblocks : n_vblocks, n_heads, s);
+    e = launch_verify<1, 8>(args, block_rows > 128 ? 2 * n_vblocks : n_vblocks, n_heads, s);
   }
   FDL_HIP_CHECK(e);
   return ok();

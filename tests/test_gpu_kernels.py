@@ -637,6 +637,35 @@ def test_verify_attention_batch16_cache1024():
     _close(_np(out), ref, what="verify attention")
 
 
+@pytest.mark.parametrize("bm", [32, 64, 128])
+def test_verify_attention_two_heads_per_workgroup_matches_one(bm):
+    """A verify grid of more than one round of workgroups (9 blocks x 32 heads, above the
+    device's CU count) runs two heads per workgroup, the second head's key blocks streaming
+    through the LDS ring behind the first head's. Every (block, head) output equals, bit for
+    bit, the one-head launch of that block alone (9 calls of one block: 32 workgroups
+    each); 64-, 128- and 256-row blocks (64-row tiles, 128-row tiles, two 128-row tiles)."""
+    H, n_blk, L = 32, 9, 512
+    key_pos, vblocks, _, _, ts = _verify_case(41 + bm, n_blk, L, H, bm, with_ts=True, s_min=1)
+    rows = 2 * bm
+    gen = torch.Generator().manual_seed(42 + bm)
+    D = H * 128
+    q, k1, v1 = (_bf16((n_blk * rows, D), gen).to(DEV) for _ in range(3))
+    kc, vc = (_bf16((n_blk * L, D), gen).to(DEV) for _ in range(2))
+    kp = torch.from_numpy(key_pos).to(DEV)
+    vb = torch.from_numpy(vblocks).to(DEV)
+    tsd = torch.from_numpy(ts).to(DEV)
+    scale = orc.softmax_scale(128)
+    out_all = torch.full((n_blk * rows, D), POISON, dtype=torch.bfloat16, device=DEV)
+    ops.verify_attention(q, k1, v1, kc, vc, kp, vb, tsd, rows, out_all, H, scale)
+    out_one = torch.full_like(out_all, POISON)
+    for j in range(n_blk):
+        ops.verify_attention(q, k1, v1, kc, vc, kp, vb[j:j + 1].contiguous(),
+                             tsd[j:j + 1].contiguous(), rows, out_one, H, scale)
+    torch.cuda.synchronize()
+    assert not torch.equal(out_all, torch.full_like(out_all, POISON))
+    assert torch.equal(out_all, out_one)
+
+
 def test_verify_end_to_end_projection_and_attention():
     """Packed verify projection followed by verify attention, as the verify pass runs them
     (flash_cache_triton.py:499-535)."""
