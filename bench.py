@@ -252,6 +252,13 @@ def _graph_time(fn, reps: int, replays: int = 3) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * replays)
 
 
+def _op_times(fn, reps: int) -> tuple[float, float]:
+    """(graph, eager) microseconds per call of fn(): `reps` calls captured in one HIP graph
+    and replayed (the in-sequence duration, without the host's launch gaps), and the mean of
+    `reps` calls launched one by one from Python."""
+    return _graph_time(fn, reps), _time_op(fn, reps)
+
+
 def run_torch_layer(reps: int = 20, seed: int = 2) -> dict:
     """The same single-layer chain with unfused PyTorch ops on the same GPU (the
     conventional path the reference's fused kernels are compared with), batched over the
@@ -434,7 +441,9 @@ def run_configs(reps: int = 10) -> dict:
     """Secondary measurements on the other single-layer workloads (bf16, d_model 4096, 32
     heads): the one-sequence 40-row layer (weight-streaming projection: HBM-bound), the
     block-table stress batch, its full-recompute tiles on their own, and the Flash-Verify
-    batch. Synthetic N(0,1) activations and N(0,0.02) weights."""
+    batch. Synthetic N(0,1) activations and N(0,0.02) weights. Each kernel: `us` = calls
+    captured in one HIP graph and replayed (the in-sequence duration, as for the layer's
+    kernels), `eager_us` = the mean of the same calls launched one by one from Python."""
     import torch
     from fdl import lib, ops
     from fdl.schedule import SeqRows, contiguous_page_table, make_plan
@@ -459,15 +468,17 @@ def run_configs(reps: int = 10) -> dict:
     att = torch.empty_like(q)
     plan1 = make_plan([SeqRows(batch=0, k_end=c1["L"], rows=np.arange(Q1))],
                       contiguous_page_table(1, c1["L"]), device=dev)
-    t_q1 = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slot, q, kc, vc, H), 3 * reps)
-    t_a1 = _time_op(lambda: ops.block_attention(q, kc, vc, plan1, att, H, scale), 3 * reps)
+    t_q1, e_q1 = _op_times(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slot, q, kc, vc, H), 3 * reps)
+    t_a1, e_a1 = _op_times(lambda: ops.block_attention(q, kc, vc, plan1, att, H, scale), 3 * reps)
     b_q1 = 3.0 * D * D * 2 + Q1 * D * 2 * 4 + Q1 * HD * 4 * 2 + Q1 * 8
     b_a1 = 2.0 * Q1 * D * 2 + 2.0 * c1["L"] * D * 2
     out["one_sequence_40_rows"] = {
         "workload": "1 sequence, 384-slot cache, 32-row masked block + 8 tracked rows",
         "qkv_rope_cache": {"us": round(t_q1, 2), "GB/s": round(b_q1 / t_q1 / 1e3, 1),
-                           "hbm_frac": round(b_q1 / t_q1 / 1e3 / PEAK_HBM_GBS, 4)},
-        "block_attention": {"us": round(t_a1, 2), "GB/s": round(b_a1 / t_a1 / 1e3, 1)},
+                           "hbm_frac": round(b_q1 / t_q1 / 1e3 / PEAK_HBM_GBS, 4),
+                           "eager_us": round(e_q1, 2)},
+        "block_attention": {"us": round(t_a1, 2), "GB/s": round(b_a1 / t_a1 / 1e3, 1),
+                            "eager_us": round(e_a1, 2)},
     }
     del kc, vc, qp
 
@@ -485,10 +496,10 @@ def run_configs(reps: int = 10) -> dict:
     imp = torch.zeros((H, st["n_slots"]), dtype=torch.float32, device=dev)
     plan = make_plan(st["seqs"], st["table"], 5, device=dev)
     plan.validate(Q, st["n_slots"])
-    t_qkv = _time_op(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
-                                                rope_row=rope_row), reps)
-    t_att = _time_op(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
-                                                 lib.IMP_RAW_LOGIT, imp), reps)
+    t_qkv, e_qkv = _op_times(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
+                                                        rope_row=rope_row), reps)
+    t_att, e_att = _op_times(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
+                                                         lib.IMP_RAW_LOGIT, imp), reps)
     qk = np.array([len(sq.rows) for sq in st["seqs"]], dtype=np.float64)
     kk = st["k_ends"].astype(np.float64)
     f_att = float((4.0 * qk * kk * D).sum())
@@ -498,19 +509,22 @@ def run_configs(reps: int = 10) -> dict:
         "workload": f"{st['NB']} sequences, caches 512-1536 keys in permuted 32-slot pages, "
                     f"{int(st['full'].sum())} full recomputes, {Q} query rows, raw-logit importance",
         "qkv_rope_cache": {"us": round(t_qkv, 2), "TFLOP/s": round(f_qkv / t_qkv / 1e6, 1),
-                           "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
+                           "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4),
+                           "eager_us": round(e_qkv, 2)},
         "block_attention": {"us": round(t_att, 2), "TFLOP/s": round(f_att / t_att / 1e6, 1),
-                            "GB/s": round(b_att / t_att / 1e3, 1)},
+                            "GB/s": round(b_att / t_att / 1e3, 1), "eager_us": round(e_att, 2)},
     }
     fseqs = [sq for sq in st["seqs"] if len(sq.rows) == sq.k_end]
     if fseqs:
         fplan = make_plan(fseqs, st["table"], 5, device=dev)
-        t_full = _time_op(lambda: ops.block_attention(q, kc, vc, fplan, att, H, scale), reps)
+        t_full, e_full = _op_times(lambda: ops.block_attention(q, kc, vc, fplan, att, H, scale),
+                                   reps)
         ff = float(sum(4.0 * sq.k_end * sq.k_end * D for sq in fseqs))
         out["block_table_stress"]["full_recompute_attention"] = {
             "sequences": len(fseqs), "us": round(t_full, 2),
             "TFLOP/s": round(ff / t_full / 1e6, 1),
-            "mfma_frac": round(ff / t_full / 1e6 / PEAK_BF16_TFLOPS, 4)}
+            "mfma_frac": round(ff / t_full / 1e6 / PEAK_BF16_TFLOPS, 4),
+            "eager_us": round(e_full, 2)}
     del kc, vc, imp
 
     # --- Flash-Verify
@@ -527,10 +541,10 @@ def run_configs(reps: int = 10) -> dict:
     mk = torch.from_numpy(vf["mask"]).to(dev)
     qs = torch.from_numpy(vf["slots"]).to(dev)
     rows = 2 * vf["BMV"]
-    t_vq = _time_op(lambda: ops.qkv_rope_cache(xv, *w, sinv, cosv, qs, qv, k1, v1, H,
-                                               kv_packed=True), reps)
-    t_va = _time_op(lambda: ops.verify_attention(qv, k1, v1, kcv, vcv, kp, vb, mk, rows, attv, H,
-                                                 scale), reps)
+    t_vq, e_vq = _op_times(lambda: ops.qkv_rope_cache(xv, *w, sinv, cosv, qs, qv, k1, v1, H,
+                                                      kv_packed=True), reps)
+    t_va, e_va = _op_times(lambda: ops.verify_attention(qv, k1, v1, kcv, vcv, kp, vb, mk, rows,
+                                                        attv, H, scale), reps)
     sk = vf["kv"].astype(np.float64)
     LC = vf["LC"]
     f_va = float((4.0 * (2 * sk) * (LC - sk + 2 * sk) * D).sum())
@@ -538,10 +552,10 @@ def run_configs(reps: int = 10) -> dict:
     out["flash_verify"] = {
         "workload": f"{vf['NV']} sequences, 1024-slot caches, {int(sk.sum())} candidates as draft "
                     f"and mask rows ({QV} packed rows)",
-        "qkv_rope_cache_packed": {"us": round(t_vq, 2)},
+        "qkv_rope_cache_packed": {"us": round(t_vq, 2), "eager_us": round(e_vq, 2)},
         "verify_attention": {"us": round(t_va, 2), "GB/s": round(b_va / t_va / 1e3, 1),
                              "hbm_frac": round(b_va / t_va / 1e3 / PEAK_HBM_GBS, 4),
-                             "TFLOP/s": round(f_va / t_va / 1e6, 1)},
+                             "TFLOP/s": round(f_va / t_va / 1e6, 1), "eager_us": round(e_va, 2)},
     }
     return out
 
