@@ -575,22 +575,33 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   }
   // the rows' Q columns of the head at column colh, and a fresh softmax state
   RowState<RB> st;
-  auto begin_head = [&](int colh) {
+  auto load_q = [&](int colh, bf16x8 (&dst)[RB][4]) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int sd = 0; sd < 4; ++sd) {
         u32x4 v = {0, 0, 0, 0};
         if (qrow[rb] >= 0) v = ld16(a.q + qrow[rb] * D + colh + 32 * sd + 8 * g);
-        qf[rb][sd] = as_bf16x8(v);
+        dst[rb][sd] = as_bf16x8(v);
       }
+  };
+  auto reset_state = [&]() {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
       st.m[rb] = -INFINITY;
       st.l[rb] = 0.f;
 #pragma unroll
       for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
-  begin_head(col0);
+  load_q(col0, qf);
+  reset_state();
+  // verify: the block's (T, S) for the closed-form mask, read once
+  int vT = 0, vS = 0;
+  if (kVerify && a.vmeta) {
+    vT = a.vmeta[2 * vb_idx];
+    vS = a.vmeta[2 * vb_idx + 1];
+  }
   const bool wave_imp = 16 * RB * wr < n_imp;
   const int imp_waves = (n_imp + 16 * RB - 1) / (16 * RB);
   float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
@@ -661,7 +672,10 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
   for (int hj = 0; hj < HPW; ++hj) {
-    if (hj > 0) begin_head(col0 + hj * kHeadDim);
+    if (hj > 0) {
+      load_q(col0 + hj * kHeadDim, qf);
+      reset_state();
+    }
     for (int s = 0; s < n_steps; ++s) {
       const int stage = stage_of(hj * n_steps + s);
       const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
@@ -673,11 +687,6 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       if (in_blk) {
         const int br = a.block_rows;
         const int j0 = kTileN * (s - n_blk);  // first in-block key of the step
-        int vT = 0, vS = 0;
-        if (a.vmeta) {
-          vT = a.vmeta[2 * vb_idx];
-          vS = a.vmeta[2 * vb_idx + 1];
-        }
         attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
           const int r = 16 * (wr * RB + rb) + l16;  // row of this workgroup
           const int rr = r + kRows * half_v;          // row of the block
