@@ -355,6 +355,12 @@ __device__ __forceinline__ void column_sums(float (&out)[4], const bf16x8 (&qf)[
 // ws_blocks records of kWsBlock floats: [row][key] probabilities, then the rows' maxima.
 constexpr int kStoreRows = 32;
 constexpr int kWsBlock = kStoreRows * kTileN + kStoreRows;
+// Up to kRegBlocks key blocks the probabilities stay on chip instead: the consumers hand each
+// block's [row][key] probabilities to the producers through LDS (two buffers by block parity,
+// rows padded to kPStride floats), and producer wave j % 4 keeps block j in registers, lane =
+// key, all kStoreRows rows (32 registers per block); the rows' maxima stay in LDS.
+constexpr int kRegBlocks = 24;
+constexpr int kPStride = kTileN + 4;
 
 // The Flash-Verify mask of a block of T fill rows, S draft rows and S mask rows (rows and
 // columns in that order; generate.py:260-269): fill rows do not see the drafts; draft i sees
@@ -380,16 +386,33 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   constexpr int kRows = 16 * RB * NC;
   constexpr int kSt = kStages;  // LDS ring depth
   __shared__ __align__(1024) uint8_t smem[kSt * kStageBytes];
-  __shared__ float imp_buf[2][NC][kTileN];  // per-wave column sums of a block, by parity
   __shared__ float lse_buf[kRows];
   __shared__ int32_t slot_buf[kSlotCache];  // cache slot of key k_begin + i
-  // raw importance: each consumer's column sums of its importance rows' Q, and the summed Q
-  // as MFMA A-operand fragments, by lane
-  __shared__ float qsum_part[kVerify ? 1 : NC][kHeadDim];
-  __shared__ u32x4 qsum_frag_buf[kVerify ? 1 : 4][64];
-  // raw importance of key k_begin + i, written to imp_part after the key loop (a consumer's
-  // global store inside the loop would wait behind the producers' loads)
-  __shared__ float raw_buf[kVerify ? 1 : kSlotCache];
+  // Per importance mode (one per launch), in one union:
+  union ImpLds {
+    // raw: each consumer's column sums of its importance rows' Q, the summed Q as MFMA
+    // A-operand fragments by lane, and the raw importance of key k_begin + i, written to
+    // imp_part after the key loop (a consumer's global store inside the loop would wait
+    // behind the producers' loads)
+    struct {
+      float qsum_part[kVerify ? 1 : NC][kHeadDim];
+      u32x4 qsum_frag[kVerify ? 1 : 4][64];
+      float raw[kVerify ? 1 : kSlotCache];
+    } raw;
+    // softmax importance, second pass over K: per-wave column sums of a block, by parity
+    float cols[2][NC][kTileN];
+    // softmax importance, probabilities on chip: a block's probabilities by parity, and
+    // every block's row maxima (after the last block: the rows' factors 2^(m_j - lse))
+    struct {
+      float p[2][kStoreRows * kPStride];
+      float m[kRegBlocks][kStoreRows];
+    } reg;
+  };
+  __shared__ ImpLds imp_lds;
+  auto& imp_buf = imp_lds.cols;
+  auto& qsum_part = imp_lds.raw.qsum_part;
+  auto& qsum_frag_buf = imp_lds.raw.qsum_frag;
+  auto& raw_buf = imp_lds.raw.raw;
 
   const int tid = threadIdx.x;
   // The wavefront index is uniform; readfirstlane makes the role test a scalar branch, so a
@@ -450,10 +473,13 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const int n_blk = (k_end - k_begin + kTileN - 1) / kTileN;
   const bool inblock = kVerify && n_rows > 0;
   const int n_ib = inblock ? (n_in + kTileN - 1) / kTileN : 0;  // in-block key steps
-  // softmax importance from the workspace (one pass) or from a second pass over K
-  // (64-row tiles only: the 128-row variant's twelve wavefronts leave too few registers)
-  const bool store = NC == 4 && imp_soft && n_imp <= kStoreRows && n_blk <= a.ws_blocks;
-  const bool two_pass = imp_soft && !store;
+  // softmax importance in one pass with the probabilities on chip (up to kRegBlocks blocks)
+  // or in the workspace, else from a second pass over K (64-row tiles only: the 128-row
+  // variant's twelve wavefronts leave too few registers)
+  const bool reg_store = NC == 4 && imp_soft && n_imp <= kStoreRows && n_blk <= kRegBlocks;
+  const bool store =
+      NC == 4 && imp_soft && !reg_store && n_imp <= kStoreRows && n_blk <= a.ws_blocks;
+  const bool two_pass = imp_soft && !store && !reg_store;
   float* ws_tile = store ? a.ws + (int64_t(a.split ? blockIdx.x >> 1 : blockIdx.x) * gridDim.y +
                                    blockIdx.y) * a.ws_blocks * kWsBlock
                          : nullptr;
@@ -502,6 +528,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     return slots_staged ? int64_t(slot_buf[n - k_begin]) : lookup(n);
   };
 
+  float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
   if (producer) {
     const int tp = tid - 64 * NC;
     if (slots_staged) {
@@ -549,13 +576,57 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       wait_vmcnt(later_loads(0, kSt - 1));  // step 0 landed (steps 0 .. kSt - 1 issued)
     }
     barrier_only();  // #1
-    for (int s = 0; s < n_all; ++s) {
+    // one step: wait for step s + 1, hand over step s, refill its stage
+    auto step = [&](int s) {
       wait_vmcnt(later_loads(s + 1, s + kSt - 1));  // step s + 1 landed
-      barrier_only();  // consumers are done with step s
+      // consumers are done with step s (and this wave's reads of earlier probabilities)
+      barrier_lds_drained();
       // step s + kSt lives in the stage of step s (a resident block's stage is kept)
       issue(s + kSt);
+    };
+    // on-chip softmax importance: producer wr keeps blocks j = wr, wr + 4, .. in pr[j / 4]
+    // (rows 0 .. kStoreRows - 1 of key k_begin + 64 j + lane); the step loop is unrolled so
+    // that every register index is static
+    constexpr int kPrSlots = kVerify ? 1 : kRegBlocks / 4;
+    float pr[kPrSlots][kVerify ? 1 : kStoreRows];
+    if (!kVerify && reg_store) {
+#pragma unroll
+      for (int s = 0; s < kRegBlocks; ++s) {
+        if (s < n_all) {
+          step(s);
+          if ((s & 3) == wr) {
+            const float* src = imp_lds.reg.p[s & 1] + lane;
+#pragma unroll
+            for (int r = 0; r < kStoreRows; ++r) pr[(s >> 2) % kPrSlots][r] = src[r * kPStride];
+          }
+        }
+      }
+    } else {
+      for (int s = 0; s < n_all; ++s) step(s);
     }
     wait_vmcnt(0);  // no load may still be writing LDS when the workgroup ends
+    if constexpr (!kVerify) {
+      if (reg_store) {
+        // the last barrier made the last block's probabilities and the rows' factors
+        // 2^(m_j - lse) visible; column sums over the importance rows in ascending row order
+#pragma unroll
+        for (int t = 0; t < kPrSlots; ++t) {
+          const int j = 4 * t + wr;  // the block in pr[t]
+          const int n = k_begin + kTileN * j + lane;
+          if (j < n_blk && n < k_end) {
+            // the factors of all rows first (uniform 16-byte reads), then the sums
+            const f32x4* cv = reinterpret_cast<const f32x4*>(imp_lds.reg.m[j]);
+            f32x4 c[kStoreRows / 4];
+#pragma unroll
+            for (int i = 0; i < kStoreRows / 4; ++i) c[i] = cv[i];
+            float acc = 0.f;
+#pragma unroll
+            for (int r = 0; r < kStoreRows; ++r) acc = __builtin_fmaf(c[r / 4][r % 4], pr[t][r], acc);
+            imp_out[slot_of(n)] = acc;
+          }
+        }
+      }
+    }
     if (store) __syncthreads();  // the consumers' workspace stores are complete
     return;
   }
@@ -604,7 +675,6 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   }
   const bool wave_imp = 16 * RB * wr < n_imp;
   const int imp_waves = (n_imp + 16 * RB - 1) / (16 * RB);
-  float* imp_out = a.imp_part ? a.imp_part + int64_t(h) * n_slots : nullptr;
   float lse_r[RB][4];
 
   // Writes the importance sums of the block of step `s` (keys from n0): each consumer
@@ -710,7 +780,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
             st, qf, kt, vt, a.scale_log2, [&](int, int kb, int ii) { return kbias[kb][ii]; },
             [&](int rb, const f32x4 (&p)[4], float m_use) {
               const int r = 16 * (wr * RB + rb) + l16;
-              if (store && r < kStoreRows) {
+              if (reg_store && r < kStoreRows) {
+                // row r, keys 16 kb + 4 g .. + 3 of block blk, for producer blk % 4
+                float* pr = imp_lds.reg.p[blk & 1] + r * kPStride;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                  *reinterpret_cast<f32x4*>(pr + 16 * kb + 4 * g) = p[kb];
+                if (g == 0) imp_lds.reg.m[blk][r] = m_use;
+              } else if (store && r < kStoreRows) {
                 // row r, keys 16 kb + 4 g .. + 3 of block blk; then the row's maximum
                 float* rec = ws_tile + int64_t(blk) * kWsBlock;
 #pragma unroll
@@ -744,6 +821,19 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
             for (int rb = 0; rb < RB; ++rb)
               lse_buf[16 * (wr * RB + rb) + l16] =
                   st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
+          }
+          if (reg_store) {
+            // each block's row maximum becomes the row's factor 2^(m_j - lse), 0 for rows
+            // past n_imp (lane group g takes blocks g, g + 4, ..), for the producers' column
+            // sums after this step
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+              const int r = 16 * (wr * RB + rb) + l16;
+              const float lse = st.l[rb] > 0.f ? st.m[rb] + log2f(st.l[rb]) : INFINITY;
+              if (r < kStoreRows)
+                for (int j = g; j < n_blk; j += 4)
+                  imp_lds.reg.m[j][r] = r < n_imp ? fast_exp2(imp_lds.reg.m[j][r] - lse) : 0.f;
+            }
           }
         }
       } else {

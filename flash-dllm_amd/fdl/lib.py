@@ -27,6 +27,8 @@ FDL_ERR_HIP = -5
 ABI_VERSION = 2  # FDL_ABI_VERSION of include/fdl.h
 # fp32 workspace per 64-key block, head and tile of softmax importance (FDL_ATTN_WS_FLOATS_PER_BLOCK)
 ATTN_WS_FLOATS_PER_BLOCK = 32 * 64 + 32
+# key blocks whose softmax-importance probabilities a tile keeps on chip (FDL_ATTN_ONCHIP_BLOCKS)
+ATTN_ONCHIP_BLOCKS = 24
 
 IMP_NONE = 0
 IMP_RAW_LOGIT = 1

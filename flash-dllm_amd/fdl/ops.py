@@ -98,13 +98,16 @@ def _class_ranges(plan: AttnPlan):
 def attention_workspace_floats(plan: AttnPlan, n_heads: int) -> int:
     """fp32 workspace that lets every importance tile of the plan keep its softmax-importance
     probabilities for one pass (fdl_block_attention's workspace; the launches of one call
-    reuse it)."""
+    reuse it). Tiles of at most ATTN_ONCHIP_BLOCKS key blocks keep them on chip: a plan
+    without longer importance tiles needs none."""
     need = 0
     for first, count, _ in _class_ranges(plan):
         if count == 0:
             continue
         w = plan.work[first:first + count]
         blocks = int(((w[:, 2] - w[:, 1] + 63) // 64).max()) if (w[:, 5] > 0).any() else 0
+        if blocks <= _lib.ATTN_ONCHIP_BLOCKS:
+            continue
         need = max(need, count * n_heads * blocks * _lib.ATTN_WS_FLOATS_PER_BLOCK)
     return need
 

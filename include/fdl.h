@@ -112,8 +112,9 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            fdl_importance_accumulate. Each sequence must have at most one tile with
  *            n_imp > 0.
  *   workspace fp32 [workspace_floats], 16-byte aligned, or NULL / 0: with
- *            FDL_IMP_SOFTMAX_COLSUM, the importance rows' probabilities (at most 32 rows) are
- *            kept here during the one pass over K/V; a tile needs
+ *            FDL_IMP_SOFTMAX_COLSUM, a 64-row tile with at most 32 importance rows
+ *            and at most FDL_ATTN_ONCHIP_BLOCKS 64-key blocks keeps their probabilities on
+ *            chip during its one pass over K/V; a longer one keeps them here: it needs
  *            FDL_ATTN_WS_FLOATS_PER_BLOCK floats per 64-key block for each head, and the room
  *            per tile is workspace_floats / (n_work * n_heads). A tile whose keys do not fit
  *            (or with more than 32 importance rows, or without a workspace) reads K a second
@@ -121,6 +122,7 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            left undefined.
  */
 #define FDL_ATTN_WS_FLOATS_PER_BLOCK (32 * 64 + 32)
+#define FDL_ATTN_ONCHIP_BLOCKS 24
 int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
                         int64_t n_q_rows, int64_t n_slots, int64_t d_model, int64_t n_heads,
                         int64_t head_dim, const int32_t* page_table, int64_t n_seq,

@@ -304,13 +304,14 @@ def test_block_attention_full_recompute_tiles(imp_mode):
 
 
 def test_block_attention_softmax_importance_store_and_two_pass():
-    """64-row tiles with softmax-colsum importance on both of the kernel's paths: the
-    probabilities kept in LDS (at most 32 importance rows and 12 key blocks: 17 rows over
-    768 keys, 32 rows over one block) and the second pass over K (16 blocks; 48 rows)."""
-    B, L, H = 4, 1024, 4
-    k_ends = [1000, 500, 768, 64]
-    n_q = [50, 60, 40, 64]
-    n_imp = [32, 48, 17, 32]
+    """64-row tiles with softmax-colsum importance on all three of the kernel's paths: the
+    probabilities kept on chip (at most 32 importance rows and 24 key blocks: 32 rows over
+    1000 keys, 17 rows over 768 keys, 32 rows over one block), in the workspace (25 blocks)
+    and the second pass over K (48 rows)."""
+    B, L, H = 5, 1664, 4
+    k_ends = [1000, 500, 768, 64, 1600]
+    n_q = [50, 60, 40, 64, 40]
+    n_imp = [32, 48, 17, 32, 32]
     seqs, blocks, mb, q0 = [], [], [], 0
     for b in range(B):
         seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
