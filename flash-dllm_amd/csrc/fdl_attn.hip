@@ -376,10 +376,11 @@ __device__ __forceinline__ bool verify_visible(int T, int S, int r, int j) {
 }
 
 // Steps of a tile, the same sequence for producers and consumers (one barrier each):
-//   [0, n_blk)          cache blocks, K and V
+//   [0, n_blk)          cache blocks, K and V (verify: after the in-block keys)
 //   [n_blk, 2 n_blk)    softmax importance without the LDS store: the cache blocks again,
 //                       K only, last block first
-//   n_blk               verify only (when the block has rows): the in-block keys
+//   verify (when the block has rows): the in-block keys first, in steps [0, n_ib) (they
+//   were just written by the projection and come from L2 while the first cache blocks load)
 template <int RB, int NC, bool kVerify, int HPW = 1>
 __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
   static_assert(HPW == 1 || (kVerify && HPW == 2), "several heads per workgroup: verify only");
@@ -489,12 +490,13 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   // first pass, which are still in LDS, and continues with the most recently read ones.
   // Block j always lives in stage j % kSt; a resident block is not loaded again.
   auto block_of = [&](int step) {
+    if constexpr (kVerify) return step - n_ib;
     return two_pass && step >= n_blk ? 2 * n_blk - 1 - step : step;
   };
   // Global step S = n_steps j + s: step s of head j. With several heads (verify: every step
   // a fresh block) step S lives in stage S % kSt.
   const int n_all = HPW * n_steps;
-  auto stage_of = [&](int step) { return (HPW > 1 ? step : block_of(step)) % kSt; };
+  auto stage_of = [&](int step) { return (HPW > 1 || kVerify ? step : block_of(step)) % kSt; };
   // DMA per producer for global step `step` (0: past the end, or a block still resident)
   auto loads = [&](int step) {
     if (step >= n_all) return 0;
@@ -545,7 +547,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       const int hj = HPW > 1 ? gs / n_steps : 0;  // head of the step
       const int s = gs - hj * n_steps;            // its step within the head
       const int colh = col0 + hj * kHeadDim;
-      const bool in_blk = kVerify && s >= n_blk;
+      const bool in_blk = kVerify && s < n_ib;
       const bool k_only = !kVerify && s >= n_blk;
       const int n0 = k_begin + kTileN * block_of(s);
 #pragma unroll
@@ -554,8 +556,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
         const int key = 4 * q + (lane >> 4);
         const uint16_t *ks, *vs;
         if (in_blk) {
-          // in-block key 64 (s - n_blk) + key: query row blk_row0 + that (checked above)
-          const int64_t r = int64_t(blk_row0) + min(kTileN * (s - n_blk) + key, n_in - 1);
+          // in-block key 64 s + key: query row blk_row0 + that (checked above)
+          const int64_t r = int64_t(blk_row0) + min(kTileN * s + key, n_in - 1);
           ks = a.kblk + r * D + colh;
           vs = a.vblk + r * D + colh;
         } else {
@@ -751,12 +753,12 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       const u32x4* kt = reinterpret_cast<const u32x4*>(smem + stage * kStageBytes);
       const uint8_t* vt = smem + stage * kStageBytes + kTileBytes;
       const bool pass2 = !kVerify && s >= n_blk;
-      const bool in_blk = kVerify && inblock && s >= n_blk;
+      const bool in_blk = kVerify && s < n_ib;
       const int n0 = k_begin + kTileN * block_of(s);
       if (two_pass && s > n_blk) flush_imp(s - 1, k_begin + kTileN * block_of(s - 1));
       if (in_blk) {
         const int br = a.block_rows;
-        const int j0 = kTileN * (s - n_blk);  // first in-block key of the step
+        const int j0 = kTileN * s;  // first in-block key of the step
         attend_block<RB>(st, qf, kt, vt, a.scale_log2, [&](int rb, int kb, int ii) {
           const int r = 16 * (wr * RB + rb) + l16;  // row of this workgroup
           const int rr = r + kRows * half_v;          // row of the block
