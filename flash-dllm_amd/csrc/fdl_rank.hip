@@ -63,11 +63,12 @@ __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
 
 // Keeps min or max of (mine, other) for element i of a compare-exchange at stride j within
 // bitonic blocks of size k: the lower element of an ascending pair keeps the minimum.
+// One 64-bit comparison and one select: mine is kept when it is the one wanted.
 __device__ __forceinline__ uint64_t cx(uint64_t mine, uint64_t other, int i, int j, int k) {
   const bool lower = (i & j) == 0;
   const bool asc = (i & k) == 0;
   const bool take_min = lower == asc;
-  return take_min ? (mine < other ? mine : other) : (mine < other ? other : mine);
+  return (mine < other) == take_min ? mine : other;
 }
 
 // One compare-exchange step (bitonic block size K, stride J) over the R keys of each thread.
