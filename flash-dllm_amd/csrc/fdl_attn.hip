@@ -32,6 +32,7 @@
 #include "fdl_device.h"
 #include "fdl_host.h"
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -87,7 +88,18 @@ struct AttnArgs {
   float scale_log2;  // softmax_scale * log2(e)
   int split;         // 1: workgroup 2i + j runs rows [128 j, 128 j + 128) of 256-row item i
   int n_items;       // long tiles: work items of the launch (grid = n_items x heads)
+  // key-split launches (no or raw importance): workgroup z of a (tile, head) takes the key
+  // blocks [z nb / kv_parts, (z + 1) nb / kv_parts) and writes its unnormalised output and
+  // (max, sum) per row into part_o (kPartFloats per (part, row-index entry, head));
+  // attn_combine_kernel merges the parts
+  float* part_o;
+  int kv_parts;      // 1: no key split
 };
+
+// Record of one row's partial result: O (128 fp32, relative to the maximum), the maximum
+// (log2 domain) and the sum, padded to a multiple of 4 floats.
+constexpr int kPartFloats = 132;
+constexpr int kMaxKvParts = 8;
 
 template <int RB>
 struct RowState {
@@ -468,6 +480,16 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   if (!kVerify && n_rows == 0) return;  // the empty upper half of a split 128-row item
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
+  if (!kVerify && a.kv_parts > 1) {
+    // this workgroup's share of the tile's key blocks
+    const int nb = (k_end - k_begin + kTileN - 1) / kTileN;
+    const int z = static_cast<int>(blockIdx.z);
+    const int j0 = z * nb / a.kv_parts, j1 = (z + 1) * nb / a.kv_parts;
+    const int kb = k_begin;
+    k_begin = kb + kTileN * j0;
+    k_end = min(k_end, kb + kTileN * j1);
+    if (k_end < k_begin) k_end = k_begin;
+  }
 
   const bool imp_raw = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_RAW_LOGIT;
   const bool imp_soft = !kVerify && n_imp > 0 && a.imp_mode == FDL_IMP_SOFTMAX_COLSUM;
@@ -694,6 +716,24 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     }
   };
   auto write_out = [&](int colh) {
+    if (!kVerify && a.kv_parts > 1) {
+      // a key split's part: the unnormalised row, its maximum and its sum
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if (qrow[rb] < 0) continue;
+        const int64_t ri = roff + 16 * (wr * RB + rb) + l16;
+        float* rec = a.part_o + ((int64_t(blockIdx.z) * a.n_row_idx + ri) * gridDim.y + h) *
+                                    kPartFloats;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+          *reinterpret_cast<f32x4*>(rec + 16 * db + 4 * g) = st.o[rb][db];
+        if (g == 0) {
+          rec[128] = st.m[rb];
+          rec[129] = st.l[rb];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       if (qrow[rb] < 0) continue;
@@ -1102,6 +1142,56 @@ __device__ __forceinline__ void long_softmax(LongState& st, f32x4 (&sc)[2][4], b
       }
 }
 
+// Merges the kv_parts partial results of every row of a key-split launch: with m* the
+// largest part maximum and w_p = 2^(m_p - m*) (0 for a part that attended nothing),
+// out = (sum_p w_p O_p) / (sum_p w_p l_p), parts in ascending order, as bf16 like the
+// unsplit kernel's rows. Grid = (work items, heads, tile rows / 8): thread t takes 4
+// columns of one row; every part's values are loaded before the first is used.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int32_t* it = a.work + 8 * blockIdx.x;
+  const int h = blockIdx.y;
+  const int roff = it[3];
+  int n_rows = it[4];
+  if (roff < 0 || int64_t(roff) + (n_rows > 0 ? n_rows : 0) > a.n_row_idx) n_rows = 0;
+  if (n_rows > a.tile_rows) n_rows = a.tile_rows;
+  const int r = 8 * blockIdx.z + (threadIdx.x >> 5), c = 4 * (threadIdx.x & 31);
+  if (r >= n_rows) return;
+  const int64_t q = a.row_idx[roff + r];
+  if (q < 0 || q >= a.n_q_rows) return;
+  const int P = a.kv_parts;
+  const int64_t stride = int64_t(a.n_row_idx) * gridDim.y * kPartFloats;  // between parts
+  const float* rec0 = a.part_o + ((int64_t(roff) + r) * gridDim.y + h) * kPartFloats;
+  float mp[kMaxKvParts], lp[kMaxKvParts];
+  f32x4 op[kMaxKvParts];
+#pragma unroll
+  for (int p = 0; p < kMaxKvParts; ++p) {
+    mp[p] = -INFINITY;
+    lp[p] = 0.f;
+    op[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (p < P) {
+      const float* rec = rec0 + p * stride;
+      mp[p] = rec[128];
+      lp[p] = rec[129];
+      op[p] = *reinterpret_cast<const f32x4*>(rec + c);
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < kMaxKvParts; ++p) m = fmaxf(m, mp[p]);
+  float l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < kMaxKvParts; ++p) {
+    const float w = mp[p] == -INFINITY ? 0.f : fast_exp2(mp[p] - m);
+    l = __builtin_fmaf(w, lp[p], l);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(w, op[p][e], o[e]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const u32x2 pk = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+  st8(a.out + q * a.d_model + h * kHeadDim + c, pk);
+}
+
 // Importance: none or raw logits (the softmax-colsum mode runs the 128-row kernel on split
 // items). Both groups execute 3 + 2 n_blk barriers.
 __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
@@ -1408,7 +1498,8 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
 template <int RB, int NC, bool kVerify>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
   hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>),
-                     dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads)),
+                     dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads),
+                          static_cast<unsigned>(args.kv_parts > 1 ? args.kv_parts : 1)),
                      dim3(64 * (NC + kProducers)), 0, s, args);
   return hipGetLastError();
 }
@@ -1506,6 +1597,26 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
   args.tile_rows = tile_rows;
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
+  // Key split: a launch of 64- or 128-row tiles whose (tile, head) grid fills at most half of
+  // the device (without softmax-colsum importance, which needs every key of a row) spreads
+  // each tile's key blocks over up to kMaxKvParts workgroups when the workspace holds their
+  // partial rows, then merges them.
+  int parts = 1;
+  if (imp_mode != FDL_IMP_SOFTMAX_COLSUM && (tile_rows == 64 || tile_rows == 128) &&
+      workspace != nullptr) {
+    const int64_t cus = attn_device_cus(), grid = n_work * n_heads;
+    if (2 * grid <= cus) {
+      const int64_t room = workspace_floats / (n_row_idx * n_heads * kPartFloats);
+      const int64_t p = std::min<int64_t>({kMaxKvParts, cus / grid, room});
+      if (p >= 2) parts = static_cast<int>(p);
+    }
+  }
+  if (parts > 1) {
+    FDL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, FDL_ERR_SHAPE,
+                "%s: workspace must be 16-byte aligned", fn);
+    args.part_o = workspace;
+    args.kv_parts = parts;
+  }
   // 64-row tiles: four consumers of 16 rows; 128-row tiles: eight consumers (two per SIMD);
   // 256-row tiles: the two-group kernel, or with softmax-colsum importance the 128-row
   // kernel on each half of an item (the importance rows lie in the first half)
@@ -1529,6 +1640,13 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
     e = hipGetLastError();
   }
   FDL_HIP_CHECK(e);
+  if (parts > 1) {
+    hipLaunchKernelGGL(attn_combine_kernel,
+                       dim3(static_cast<unsigned>(n_work), static_cast<unsigned>(n_heads),
+                            static_cast<unsigned>(tile_rows / 8)),
+                       dim3(256), 0, s, args);
+    FDL_HIP_CHECK(hipGetLastError());
+  }
   return FDL_OK;
 }
 

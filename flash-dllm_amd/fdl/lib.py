@@ -29,6 +29,10 @@ ABI_VERSION = 2  # FDL_ABI_VERSION of include/fdl.h
 ATTN_WS_FLOATS_PER_BLOCK = 32 * 64 + 32
 # key blocks whose softmax-importance probabilities a tile keeps on chip (FDL_ATTN_ONCHIP_BLOCKS)
 ATTN_ONCHIP_BLOCKS = 24
+# key-split attention: floats per (part, row-index entry, head) and the most parts per tile
+# (FDL_ATTN_PART_FLOATS, FDL_ATTN_MAX_KV_PARTS)
+ATTN_PART_FLOATS = 132
+ATTN_MAX_KV_PARTS = 8
 
 IMP_NONE = 0
 IMP_RAW_LOGIT = 1

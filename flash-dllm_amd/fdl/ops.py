@@ -112,14 +112,42 @@ def attention_workspace_floats(plan: AttnPlan, n_heads: int) -> int:
     return need
 
 
+_cu_count: dict = {}
+
+
+def _cus(dev: torch.device) -> int:
+    n = _cu_count.get(dev.index)
+    if n is None:
+        n = _cu_count[dev.index] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return n
+
+
+def attention_split_floats(plan: AttnPlan, n_heads: int, cus: int) -> int:
+    """fp32 workspace for fdl_block_attention's key split (no or raw importance): a class of
+    64- or 128-row tiles whose n_work * n_heads workgroups fill at most half of the `cus`
+    compute units spreads each tile's keys over min(ATTN_MAX_KV_PARTS, cus // (n_work *
+    n_heads)) workgroups, each writing ATTN_PART_FLOATS floats per row-index entry and head."""
+    n_row_idx = max(int(plan.row_idx.size), 1)
+    need = 0
+    for _, count, tile_rows in _class_ranges(plan):
+        if count == 0 or tile_rows == LONG_TILE_ROWS or 2 * count * n_heads > cus:
+            continue
+        parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads))
+        if parts >= 2:
+            need = max(need, parts * n_row_idx * n_heads * _lib.ATTN_PART_FLOATS)
+    return need
+
+
 def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     plan: AttnPlan, out: torch.Tensor, n_heads: int, softmax_scale: float,
                     imp_mode: int = _lib.IMP_NONE, imp_part: torch.Tensor | None = None,
-                    workspace: torch.Tensor | None = None) -> None:
+                    workspace: torch.Tensor | None = None, key_split: bool = True) -> None:
     """Block-table attention with the importance side output (fdl_block_attention). With
     softmax-colsum importance a float32 `workspace` of attention_workspace_floats(plan,
-    n_heads) elements keeps the importance rows' probabilities (allocated from torch's
-    caching allocator when not given)."""
+    n_heads) elements keeps the importance rows' probabilities; without, one of
+    attention_split_floats(plan, n_heads, CUs) elements holds the partial rows of a key split
+    (a launch that would fill at most half of the device). Allocated from torch's caching
+    allocator when not given; key_split=False runs every tile in one workgroup per head."""
     dev = q.device
     _need(q, "q", BF16, 2)
     _need(k_cache, "k_cache", BF16, 2, dev)
@@ -145,6 +173,10 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     if imp_mode == _lib.IMP_SOFTMAX_COLSUM and workspace is None:
         workspace = torch.empty(max(attention_workspace_floats(plan, n_heads), 4),
                                 dtype=torch.float32, device=dev)
+    elif imp_mode != _lib.IMP_SOFTMAX_COLSUM and workspace is None and key_split:
+        n = attention_split_floats(plan, n_heads, _cus(dev))
+        if n:
+            workspace = torch.empty(n, dtype=torch.float32, device=dev)
     if workspace is not None:
         _need(workspace, "workspace", torch.float32, 1, dev)
     # long tiles (the first n_long work items), mid tiles (the next n_mid), short tiles

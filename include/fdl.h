@@ -118,11 +118,19 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            FDL_ATTN_WS_FLOATS_PER_BLOCK floats per 64-key block for each head, and the room
  *            per tile is workspace_floats / (n_work * n_heads). A tile whose keys do not fit
  *            (or with more than 32 importance rows, or without a workspace) reads K a second
- *            time instead; the results are the same. Contents need no initialisation and are
- *            left undefined.
+ *            time instead; the results are the same. Without softmax-colsum importance, a
+ *            call of 64- or 128-row tiles whose n_work * n_heads workgroups fill at most half
+ *            of the device's compute units splits every tile's key blocks over
+ *            p = min(FDL_ATTN_MAX_KV_PARTS, CUs / (n_work * n_heads)) workgroups when the
+ *            workspace holds p * n_row_idx * n_heads * FDL_ATTN_PART_FLOATS floats (fewer
+ *            parts fit otherwise; none without a workspace), and merges their partial rows
+ *            in a second kernel: same attention within rounding, raw importance unchanged.
+ *            Contents need no initialisation and are left undefined.
  */
 #define FDL_ATTN_WS_FLOATS_PER_BLOCK (32 * 64 + 32)
 #define FDL_ATTN_ONCHIP_BLOCKS 24
+#define FDL_ATTN_PART_FLOATS 132
+#define FDL_ATTN_MAX_KV_PARTS 8
 int fdl_block_attention(const void* q, const void* k_cache, const void* v_cache,
                         int64_t n_q_rows, int64_t n_slots, int64_t d_model, int64_t n_heads,
                         int64_t head_dim, const int32_t* page_table, int64_t n_seq,

@@ -410,6 +410,50 @@ def test_verify_attention_key_list_beyond_the_staged_slot_map():
     _close(_np(out), ref, what="verify attention, long key lists")
 
 
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT])
+@pytest.mark.parametrize("case", ["one_sequence_384", "ragged_3"])
+def test_block_attention_key_split_matches_one_workgroup(imp_mode, case):
+    """A launch that fills at most half of the device splits every tile's key blocks over
+    several workgroups and merges their rows: one sequence of 40 rows over 384 keys with 32
+    heads (eight parts for six blocks, two of them empty), and three sequences over 1000,
+    130 and 64 keys with 8 heads (eight parts: two blocks each, mostly empty parts). The
+    output agrees with the unsplit launch within bf16 rounding and with the oracle; the raw
+    importance is bit-identical (each key's sum is formed by one workgroup either way)."""
+    if case == "one_sequence_384":
+        H, L, k_ends, n_q, n_imp = 32, 384, [384], [40], [32]
+    else:
+        H, L, k_ends, n_q, n_imp = 8, 1024, [1000, 130, 64], [50, 33, 64], [32, 17, 32]
+    B = len(k_ends)
+    seqs, blocks, q0 = [], [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
+                            n_imp=n_imp[b] if imp_mode else 0))
+        blocks.append((b, k_ends[b], q0, q0 + n_q[b]))
+        q0 += n_q[b]
+    Q = q0
+    q, kc, vc = _attn_inputs(31, Q, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert ops.attention_split_floats(plan, H, cus) > 0  # the launch does split
+    scale = orc.softmax_scale(128)
+    outs, imps = [], []
+    for split in (True, False):
+        out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+        imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV)
+        ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode,
+                            imp if imp_mode else None, key_split=split)
+        torch.cuda.synchronize()
+        outs.append(_np(out))
+        imps.append(imp.cpu())
+    np.testing.assert_allclose(outs[0], outs[1], atol=1e-2, rtol=1e-2, err_msg="split vs unsplit")
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    _close(outs[0], orc.block_attention(qn, kn, vn, np.array(blocks), L, H, scale),
+           what="split attention out")
+    if imp_mode:
+        assert torch.equal(imps[0], imps[1])
+
+
 def test_block_attention_leaves_other_rows_untouched():
     B, L, H = 2, 128, 2
     seqs = [SeqRows(0, 100, np.array([5, 1, 9])), SeqRows(1, 128, np.array([0, 7]))]
