@@ -182,6 +182,33 @@ def test_build_work_tile_classes():
         build_work([SeqRows(0, 64, np.arange(0, 10), 11)])
 
 
+def test_attention_workspace_sizes():
+    """Key-split workspace: a class whose tiles x heads fill at most half of the compute
+    units gets min(8, CUs / (tiles x heads)) parts of ATTN_PART_FLOATS per row-index entry
+    and head, the 256-row class none; softmax-importance workspace only past
+    ATTN_ONCHIP_BLOCKS key blocks. The constants match the header's."""
+    from fdl import ops
+    from fdl.schedule import make_plan
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "fdl.h").read_text()
+    for name in ("ATTN_PART_FLOATS", "ATTN_MAX_KV_PARTS", "ATTN_ONCHIP_BLOCKS"):
+        m = re.search(rf"#define FDL_{name} (\d+)", hdr)
+        assert m and int(m.group(1)) == getattr(lib, name), name
+    one = make_plan([SeqRows(0, 384, np.arange(40), 0)], contiguous_page_table(1, 384))
+    assert ops.attention_split_floats(one, 32, 256) == 8 * 40 * 32 * lib.ATTN_PART_FLOATS
+    assert ops.attention_split_floats(one, 32, 96) == 3 * 40 * 32 * lib.ATTN_PART_FLOATS
+    assert ops.attention_split_floats(one, 32, 63) == 0  # 32 workgroups fill more than half
+    three = make_plan([SeqRows(b, 1024, np.arange(64 * b, 64 * b + 64), 0) for b in range(3)],
+                      contiguous_page_table(3, 1024))
+    assert ops.attention_split_floats(three, 32, 256) == 2 * 192 * 32 * lib.ATTN_PART_FLOATS
+    assert ops.attention_split_floats(three, 64, 256) == 0  # 192 workgroups: no split
+    full = make_plan([SeqRows(0, 600, np.arange(600), 0)], contiguous_page_table(1, 640))
+    assert ops.attention_split_floats(full, 32, 256) == 0  # long tiles only
+    soft = make_plan([SeqRows(0, 1536, np.arange(64), 32)], contiguous_page_table(1, 1536))
+    assert ops.attention_workspace_floats(soft, 32) == 0  # 24 blocks: on chip
+    soft = make_plan([SeqRows(0, 1600, np.arange(64), 32)], contiguous_page_table(1, 1600))
+    assert ops.attention_workspace_floats(soft, 32) == 32 * 25 * lib.ATTN_WS_FLOATS_PER_BLOCK
+
+
 def test_validate_work():
     pt = contiguous_page_table(2, 128)
     work, rows, n_long, n_mid = build_work([SeqRows(0, 100, np.arange(0, 40), 8),
