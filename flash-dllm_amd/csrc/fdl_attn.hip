@@ -393,9 +393,12 @@ __device__ __forceinline__ bool verify_visible(int T, int S, int r, int j) {
 //                       K only, last block first
 //   verify (when the block has rows): the in-block keys first, in steps [0, n_ib) (they
 //   were just written by the projection and come from L2 while the first cache blocks load)
-template <int RB, int NC, bool kVerify, int HPW = 1>
+// kSplit: a key-split launch (grid z = part; a.kv_parts > 1), a separate instance so that
+// the unsplit kernels keep their code.
+template <int RB, int NC, bool kVerify, int HPW = 1, bool kSplit = false>
 __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArgs a) {
   static_assert(HPW == 1 || (kVerify && HPW == 2), "several heads per workgroup: verify only");
+  static_assert(!kSplit || (!kVerify && HPW == 1), "key split: block attention only");
   constexpr int kRows = 16 * RB * NC;
   constexpr int kSt = kStages;  // LDS ring depth
   __shared__ __align__(1024) uint8_t smem[kSt * kStageBytes];
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   if (!kVerify && n_rows == 0) return;  // the empty upper half of a split 128-row item
   if (n_imp > n_rows) n_imp = n_rows;
   if (k_end < k_begin) k_end = k_begin;
-  if (!kVerify && a.kv_parts > 1) {
+  if constexpr (kSplit) {
     // this workgroup's share of the tile's key blocks
     const int nb = (k_end - k_begin + kTileN - 1) / kTileN;
     const int z = static_cast<int>(blockIdx.z);
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     }
   };
   auto write_out = [&](int colh) {
-    if (!kVerify && a.kv_parts > 1) {
+    if constexpr (kSplit) {
       // a key split's part: the unnormalised row, its maximum and its sum
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -1497,10 +1500,17 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
 
 template <int RB, int NC, bool kVerify>
 hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>),
-                     dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads),
-                          static_cast<unsigned>(args.kv_parts > 1 ? args.kv_parts : 1)),
-                     dim3(64 * (NC + kProducers)), 0, s, args);
+  const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads));
+  if constexpr (!kVerify) {
+    if (args.kv_parts > 1) {
+      hipLaunchKernelGGL((attn_kernel<RB, NC, false, 1, true>),
+                         dim3(grid.x, grid.y, static_cast<unsigned>(args.kv_parts)),
+                         dim3(64 * (NC + kProducers)), 0, s, args);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>), grid, dim3(64 * (NC + kProducers)), 0, s,
+                     args);
   return hipGetLastError();
 }
 
@@ -1597,18 +1607,19 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
   args.tile_rows = tile_rows;
   args.imp_mode = imp_mode;
   args.scale_log2 = softmax_scale * kLog2e;
-  // Key split: a launch of 64- or 128-row tiles whose (tile, head) grid fills at most half of
-  // the device (without softmax-colsum importance, which needs every key of a row) spreads
-  // each tile's key blocks over up to kMaxKvParts workgroups when the workspace holds their
-  // partial rows, then merges them.
+  // Key split: a launch of 64- or 128-row tiles whose (tile, head) grid fills at most a
+  // quarter of the device (without softmax-colsum importance, which needs every key of a
+  // row) spreads each tile's key blocks over 4 to kMaxKvParts workgroups when the workspace
+  // holds their partial rows, then merges them (two parts on a half-filled device cost more
+  // than they save).
   int parts = 1;
   if (imp_mode != FDL_IMP_SOFTMAX_COLSUM && (tile_rows == 64 || tile_rows == 128) &&
       workspace != nullptr) {
     const int64_t cus = attn_device_cus(), grid = n_work * n_heads;
-    if (2 * grid <= cus) {
+    if (4 * grid <= cus) {
       const int64_t room = workspace_floats / (n_row_idx * n_heads * kPartFloats);
       const int64_t p = std::min<int64_t>({kMaxKvParts, cus / grid, room});
-      if (p >= 2) parts = static_cast<int>(p);
+      if (p >= 4) parts = static_cast<int>(p);
     }
   }
   if (parts > 1) {

@@ -124,16 +124,16 @@ def _cus(dev: torch.device) -> int:
 
 def attention_split_floats(plan: AttnPlan, n_heads: int, cus: int) -> int:
     """fp32 workspace for fdl_block_attention's key split (no or raw importance): a class of
-    64- or 128-row tiles whose n_work * n_heads workgroups fill at most half of the `cus`
+    64- or 128-row tiles whose n_work * n_heads workgroups fill at most a quarter of the `cus`
     compute units spreads each tile's keys over min(ATTN_MAX_KV_PARTS, cus // (n_work *
     n_heads)) workgroups, each writing ATTN_PART_FLOATS floats per row-index entry and head."""
     n_row_idx = max(int(plan.row_idx.size), 1)
     need = 0
     for _, count, tile_rows in _class_ranges(plan):
-        if count == 0 or tile_rows == LONG_TILE_ROWS or 2 * count * n_heads > cus:
+        if count == 0 or tile_rows == LONG_TILE_ROWS or 4 * count * n_heads > cus:
             continue
         parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads))
-        if parts >= 2:
+        if parts >= 4:
             need = max(need, parts * n_row_idx * n_heads * _lib.ATTN_PART_FLOATS)
     return need
 
@@ -146,7 +146,7 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     softmax-colsum importance a float32 `workspace` of attention_workspace_floats(plan,
     n_heads) elements keeps the importance rows' probabilities; without, one of
     attention_split_floats(plan, n_heads, CUs) elements holds the partial rows of a key split
-    (a launch that would fill at most half of the device). Allocated from torch's caching
+    (a launch that would fill at most a quarter of the device). Allocated from torch's caching
     allocator when not given; key_split=False runs every tile in one workgroup per head."""
     dev = q.device
     _need(q, "q", BF16, 2)

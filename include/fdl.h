@@ -119,11 +119,11 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            per tile is workspace_floats / (n_work * n_heads). A tile whose keys do not fit
  *            (or with more than 32 importance rows, or without a workspace) reads K a second
  *            time instead; the results are the same. Without softmax-colsum importance, a
- *            call of 64- or 128-row tiles whose n_work * n_heads workgroups fill at most half
- *            of the device's compute units splits every tile's key blocks over
+ *            call of 64- or 128-row tiles whose n_work * n_heads workgroups fill at most a
+ *            quarter of the device's compute units splits every tile's key blocks over
  *            p = min(FDL_ATTN_MAX_KV_PARTS, CUs / (n_work * n_heads)) workgroups when the
  *            workspace holds p * n_row_idx * n_heads * FDL_ATTN_PART_FLOATS floats (fewer
- *            parts fit otherwise; none without a workspace), and merges their partial rows
+ *            parts when it holds less, none below 4 or without a workspace), and merges their partial rows
  *            in a second kernel: same attention within rounding, raw importance unchanged.
  *            Contents need no initialisation and are left undefined.
  */

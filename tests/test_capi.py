@@ -183,9 +183,9 @@ def test_build_work_tile_classes():
 
 
 def test_attention_workspace_sizes():
-    """Key-split workspace: a class whose tiles x heads fill at most half of the compute
-    units gets min(8, CUs / (tiles x heads)) parts of ATTN_PART_FLOATS per row-index entry
-    and head, the 256-row class none; softmax-importance workspace only past
+    """Key-split workspace: a class whose tiles x heads fill at most a quarter of the
+    compute units gets min(8, CUs / (tiles x heads)) parts of ATTN_PART_FLOATS per row-index
+    entry and head, the 256-row class none; softmax-importance workspace only past
     ATTN_ONCHIP_BLOCKS key blocks. The constants match the header's."""
     from fdl import ops
     from fdl.schedule import make_plan
@@ -195,12 +195,12 @@ def test_attention_workspace_sizes():
         assert m and int(m.group(1)) == getattr(lib, name), name
     one = make_plan([SeqRows(0, 384, np.arange(40), 0)], contiguous_page_table(1, 384))
     assert ops.attention_split_floats(one, 32, 256) == 8 * 40 * 32 * lib.ATTN_PART_FLOATS
-    assert ops.attention_split_floats(one, 32, 96) == 3 * 40 * 32 * lib.ATTN_PART_FLOATS
-    assert ops.attention_split_floats(one, 32, 63) == 0  # 32 workgroups fill more than half
+    assert ops.attention_split_floats(one, 32, 160) == 5 * 40 * 32 * lib.ATTN_PART_FLOATS
+    assert ops.attention_split_floats(one, 32, 127) == 0  # 32 workgroups: over a quarter
     three = make_plan([SeqRows(b, 1024, np.arange(64 * b, 64 * b + 64), 0) for b in range(3)],
                       contiguous_page_table(3, 1024))
-    assert ops.attention_split_floats(three, 32, 256) == 2 * 192 * 32 * lib.ATTN_PART_FLOATS
-    assert ops.attention_split_floats(three, 64, 256) == 0  # 192 workgroups: no split
+    assert ops.attention_split_floats(three, 16, 256) == 5 * 192 * 16 * lib.ATTN_PART_FLOATS
+    assert ops.attention_split_floats(three, 32, 256) == 0  # 96 workgroups: two parts only
     full = make_plan([SeqRows(0, 600, np.arange(600), 0)], contiguous_page_table(1, 640))
     assert ops.attention_split_floats(full, 32, 256) == 0  # long tiles only
     soft = make_plan([SeqRows(0, 1536, np.arange(64), 32)], contiguous_page_table(1, 1536))
