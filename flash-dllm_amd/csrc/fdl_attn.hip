@@ -1292,16 +1292,17 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
   // slots come from one page-table entry.
   const bool scalar_pages = (k_begin & 7) == 0 && pl >= 3;
   const int64_t slot_last = n_blk > 0 ? lookup(k_end - 1) : 0;
-  auto issue = [&](int blk) {
+  // the share of wavefront w (uniform) of block blk
+  auto issue = [&](int blk, int w) {
     const uint32_t st_lds = smem_lds + uint32_t((blk % kLongStages) * kStageBytes);
     const int n0 = k_begin + kTileN * blk;
     int64_t slots[2];
     if (slots_staged) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        slots[i] = slot_buf[min(n0 + 8 * wave + 4 * i + (lane >> 4), k_end - 1) - k_begin];
+        slots[i] = slot_buf[min(n0 + 8 * w + 4 * i + (lane >> 4), k_end - 1) - k_begin];
     } else if (scalar_pages) {
-      const int nf = __builtin_amdgcn_readfirstlane(n0 + 8 * wave);
+      const int nf = __builtin_amdgcn_readfirstlane(n0 + 8 * w);
       const int64_t base = nf < k_end ? int64_t(ptab[nf >> pl]) << pl : 0;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -1312,11 +1313,11 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        slots[i] = slot_of(min(n0 + 8 * wave + 4 * i + (lane >> 4), k_end - 1));
+        slots[i] = slot_of(min(n0 + 8 * w + 4 * i + (lane >> 4), k_end - 1));
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int q = 2 * wave + i;
+      const int q = 2 * w + i;
       const int key = 4 * q + (lane >> 4);
       const uint16_t* ks = a.k + slots[i] * D + col0;
       const uint16_t* vs = a.v + slots[i] * D + col0;
@@ -1346,12 +1347,22 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
 
   {
     const int np = min(n_blk, kLongStages);
-    for (int blk = 0; blk < np; ++blk) issue(blk);
+    for (int blk = 0; blk < np; ++blk) issue(blk, wave);
     if (np > 0) wait_loads(kLongLoads * (np - 1));  // block 0 landed
   }
-  // at the end of pair p each wave waits for its share of block p + 1 (block p + 2 may still
-  // be in flight); the barrier that follows hands block p + 1 to all readers
-  auto wait_next = [&](int p) { wait_loads(p + 2 < n_blk ? kLongLoads : 0); };
+  // Blocks past the first kLongStages are loaded by group A alone, both halves, in its
+  // softmax phase (next to group B's MFMA phase, the longer one): group B's softmax phase
+  // then holds no load issue, which stalls while the load queue is full.
+  // At the end of pair p each wave waits for its loads of block p + 1 (block p + 2 may still
+  // be in flight); the barrier that follows hands block p + 1 to all readers. Group A: one
+  // share of block 1 (p = 0), both shares of later blocks; group B: only its shares of the
+  // first kLongStages blocks.
+  auto wait_next = [&](int p) {
+    if (grp_a)
+      wait_loads(p + 2 < n_blk ? (p == 0 ? kLongLoads : 2 * kLongLoads) : 0);
+    else
+      wait_loads(p == 0 && n_blk > 2 ? kLongLoads : 0);
+  };
   barrier_only();
   if (n_blk > 0) {
     f32x4 sc[2][4];
@@ -1390,9 +1401,13 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
           long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
           imp_block(p);
           barrier_only();
-          if (p + 2 < n_blk) issue(p + 2);  // into the stage of block p - 1, released in pair p - 1
+          // into the stage of block p - 1, released in pair p - 1: one share before the
+          // softmax, the other after the transpose (each issue may wait for room in the
+          // load queue)
+          if (p + 2 < n_blk) issue(p + 2, wave);
           long_softmax<false>(st, sc, pb, sl2, kTileN, g);
           transpose(p);
+          if (p + 2 < n_blk) issue(p + 2, wave + 4);
           wait_next(p);
           barrier_only();
         }
@@ -1419,7 +1434,6 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
       if (n_blk > 1) wait_next(0);
       barrier_only();
       for (int p = 1; p < n_blk; ++p) {
-        if (p + 2 < n_blk) issue(p + 2);
         long_softmax<false>(st, sc, pb, sl2, kTileN, g);
         barrier_only();
         long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
