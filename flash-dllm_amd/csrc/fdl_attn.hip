@@ -88,6 +88,8 @@ struct AttnArgs {
   float scale_log2;  // softmax_scale * log2(e)
   int split;         // 1: workgroup 2i + j runs rows [128 j, 128 j + 128) of 256-row item i
   int n_items;       // long tiles: work items of the launch (grid = n_items x heads)
+  int head_groups;   // attn_kernel: groups of HPW heads; workgroup i runs head group
+                     // i % head_groups of tile i / head_groups
   // key-split launches (no or raw importance): workgroup z of a (tile, head) takes the key
   // blocks [z nb / kv_parts, (z + 1) nb / kv_parts) and writes its unnormalised output and
   // (max, sum) per row into part_o (kPartFloats per (part, row-index entry, head));
@@ -437,9 +439,14 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const bool producer = wave >= NC;
   const int wr = producer ? wave - NC : wave;  // producer index or consumer index
   const int l16 = lane & 15, g = lane >> 4;
-  // heads h .. h + HPW - 1, one after the other: the key steps of every head run through
-  // the same LDS ring, so the next head's first blocks load while this head finishes
-  const int h = blockIdx.y * HPW;
+  // The grid is tile-major with the head group fastest, so workgroups start in work-list
+  // order (longest tiles first) across all heads: a launch of several rounds ends with the
+  // shortest tiles. Heads h .. h + HPW - 1, one after the other: the key steps of every
+  // head run through the same LDS ring, so the next head's first blocks load while this
+  // head finishes.
+  const int tile = static_cast<int>(blockIdx.x / unsigned(a.head_groups));
+  const int hg = static_cast<int>(blockIdx.x - unsigned(tile) * unsigned(a.head_groups));
+  const int h = hg * HPW;
   const int64_t D = a.d_model;
   const int col0 = h * kHeadDim;
 
@@ -448,8 +455,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   // are also its in-block keys)
   int vb_idx = 0, half_v = 0, blk_row0 = 0, n_in = 0;
   if constexpr (kVerify) {
-    vb_idx = a.split ? int(blockIdx.x >> 1) : int(blockIdx.x);
-    half_v = a.split ? int(blockIdx.x & 1) : 0;
+    vb_idx = a.split ? tile >> 1 : tile;
+    half_v = a.split ? tile & 1 : 0;
     const int32_t* vb = a.vblocks + 4 * vb_idx;
     k_begin = vb[0];
     k_end = vb[1];
@@ -463,8 +470,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
     n_rows = n_in - kRows * half_v;
     if (a.split && n_rows <= 0) return;  // an empty upper half
   } else {
-    const int half = a.split ? int(blockIdx.x & 1) : 0;
-    const int32_t* it = a.work + 8 * (a.split ? blockIdx.x >> 1 : blockIdx.x);
+    const int half = a.split ? tile & 1 : 0;
+    const int32_t* it = a.work + 8 * (a.split ? tile >> 1 : tile);
     b = it[0];
     k_begin = it[1];
     k_end = it[2];
@@ -506,8 +513,8 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   const bool store =
       NC == 4 && imp_soft && !reg_store && n_imp <= kStoreRows && n_blk <= a.ws_blocks;
   const bool two_pass = imp_soft && !store && !reg_store;
-  float* ws_tile = store ? a.ws + (int64_t(a.split ? blockIdx.x >> 1 : blockIdx.x) * gridDim.y +
-                                   blockIdx.y) * a.ws_blocks * kWsBlock
+  float* ws_tile = store ? a.ws + (int64_t(a.split ? tile >> 1 : tile) * a.head_groups + hg) *
+                                   a.ws_blocks * kWsBlock
                          : nullptr;
   const int n_steps = n_blk * (two_pass ? 2 : 1) + n_ib;
   // Step -> key block: the first pass walks the blocks forward, the second (softmax
@@ -725,7 +732,7 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
       for (int rb = 0; rb < RB; ++rb) {
         if (qrow[rb] < 0) continue;
         const int64_t ri = roff + 16 * (wr * RB + rb) + l16;
-        float* rec = a.part_o + ((int64_t(blockIdx.z) * a.n_row_idx + ri) * gridDim.y + h) *
+        float* rec = a.part_o + ((int64_t(blockIdx.z) * a.n_row_idx + ri) * a.head_groups + h) *
                                     kPartFloats;
 #pragma unroll
         for (int db = 0; db < 8; ++db)
@@ -1512,19 +1519,23 @@ int check_common(const char* fn, const void* q, const void* k_cache, const void*
   return FDL_OK;
 }
 
-template <int RB, int NC, bool kVerify>
-hipError_t launch_attn(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads));
+// One workgroup per (tile, group of HPW heads), the head group fastest (see attn_kernel).
+template <int RB, int NC, bool kVerify, int HPW = 1>
+hipError_t launch_attn(AttnArgs args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
+  const int64_t groups = n_heads / HPW;
+  if (n_tiles * groups >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  args.head_groups = static_cast<int>(groups);
+  const dim3 grid(static_cast<unsigned>(n_tiles * groups));
   if constexpr (!kVerify) {
     if (args.kv_parts > 1) {
       hipLaunchKernelGGL((attn_kernel<RB, NC, false, 1, true>),
-                         dim3(grid.x, grid.y, static_cast<unsigned>(args.kv_parts)),
+                         dim3(grid.x, 1, static_cast<unsigned>(args.kv_parts)),
                          dim3(64 * (NC + kProducers)), 0, s, args);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify>), grid, dim3(64 * (NC + kProducers)), 0, s,
-                     args);
+  hipLaunchKernelGGL((attn_kernel<RB, NC, kVerify, HPW>), grid, dim3(64 * (NC + kProducers)), 0,
+                     s, args);
   return hipGetLastError();
 }
 
@@ -1549,12 +1560,8 @@ int attn_device_cus() {
 // round's start-up.
 template <int RB, int NC>
 hipError_t launch_verify(const AttnArgs& args, int64_t n_tiles, int64_t n_heads, hipStream_t s) {
-  if (n_heads % 2 == 0 && n_tiles * n_heads > attn_device_cus()) {
-    hipLaunchKernelGGL((attn_kernel<RB, NC, true, 2>),
-                       dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_heads / 2)),
-                       dim3(64 * (NC + kProducers)), 0, s, args);
-    return hipGetLastError();
-  }
+  if (n_heads % 2 == 0 && n_tiles * n_heads > attn_device_cus())
+    return launch_attn<RB, NC, true, 2>(args, n_tiles, n_heads, s);
   return launch_attn<RB, NC, true>(args, n_tiles, n_heads, s);
 }
 
