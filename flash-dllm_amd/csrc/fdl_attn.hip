@@ -701,6 +701,10 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   };
   load_q(col0, qf);
   reset_state();
+  // with several heads per workgroup the next head's Q columns load one head ahead, so the
+  // consumers do not wait on them when the head changes
+  bf16x8 qn[RB][4];
+  if constexpr (HPW > 1) load_q(col0 + kHeadDim, qn);
   // verify: the block's (T, S) for the closed-form mask, read once
   int vT = 0, vS = 0;
   if (kVerify && a.vmeta) {
@@ -794,9 +798,15 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
   barrier_lds_drained();  // #1: step 0 landed; summed-Q fragments stored
   bool l_reduced = false;  // st.l holds per-lane partial sums until reduced across lanes
   for (int hj = 0; hj < HPW; ++hj) {
-    if (hj > 0) {
-      load_q(col0 + hj * kHeadDim, qf);
-      reset_state();
+    if constexpr (HPW > 1) {
+      if (hj > 0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int sd = 0; sd < 4; ++sd) qf[rb][sd] = qn[rb][sd];
+        if (hj + 1 < HPW) load_q(col0 + (hj + 1) * kHeadDim, qn);
+        reset_state();
+      }
     }
     for (int s = 0; s < n_steps; ++s) {
       const int stage = stage_of(hj * n_steps + s);
