@@ -122,19 +122,34 @@ def _cus(dev: torch.device) -> int:
     return n
 
 
+def _split_parts(plan: AttnPlan, first: int, count: int, tile_rows: int, n_heads: int,
+                 cus: int) -> int:
+    """Key-split parts of one tile class (0: none): a class of 64- or 128-row tiles whose
+    count * n_heads workgroups fill at most a quarter of the `cus` compute units spreads each
+    tile's key blocks over min(ATTN_MAX_KV_PARTS, cus // (count * n_heads), its largest
+    tile's block count) workgroups, if that is at least four (fewer cost more than they
+    save; more than the blocks would leave parts empty). A plan built on the device has no
+    host copy of its tiles: no block cap then."""
+    if count == 0 or tile_rows == LONG_TILE_ROWS or 4 * count * n_heads > cus:
+        return 0
+    w = plan.work[first:first + count]
+    blocks = _lib.ATTN_MAX_KV_PARTS
+    if w.shape[0] == count:
+        blocks = int(((w[:, 2].astype(np.int64) - w[:, 1] + 63) // 64).max())
+    parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads), blocks)
+    return parts if parts >= 4 else 0
+
+
 def attention_split_floats(plan: AttnPlan, n_heads: int, cus: int) -> int:
-    """fp32 workspace for fdl_block_attention's key split (no or raw importance): a class of
-    64- or 128-row tiles whose n_work * n_heads workgroups fill at most a quarter of the `cus`
-    compute units spreads each tile's keys over min(ATTN_MAX_KV_PARTS, cus // (n_work *
-    n_heads)) workgroups, each writing ATTN_PART_FLOATS floats per row-index entry and head."""
+    """fp32 workspace for fdl_block_attention's key split (no or raw importance): the largest
+    class need of _split_parts workgroups per tile, each writing ATTN_PART_FLOATS floats per
+    row-index entry and head. fdl_block_attention takes its part count from the room it is
+    given, so block_attention hands each class only its own parts' room."""
     n_row_idx = max(int(plan.row_idx.size), 1)
     need = 0
-    for _, count, tile_rows in _class_ranges(plan):
-        if count == 0 or tile_rows == LONG_TILE_ROWS or 4 * count * n_heads > cus:
-            continue
-        parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads))
-        if parts >= 4:
-            need = max(need, parts * n_row_idx * n_heads * _lib.ATTN_PART_FLOATS)
+    for first, count, tile_rows in _class_ranges(plan):
+        parts = _split_parts(plan, first, count, tile_rows, n_heads, cus)
+        need = max(need, parts * n_row_idx * n_heads * _lib.ATTN_PART_FLOATS)
     return need
 
 
@@ -180,16 +195,23 @@ def block_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     if workspace is not None:
         _need(workspace, "workspace", torch.float32, 1, dev)
     # long tiles (the first n_long work items), mid tiles (the next n_mid), short tiles
+    cus = _cus(dev)
     for first, count, tile_rows in _class_ranges(plan):
         if count == 0:
             continue
+        ws_n = 0 if workspace is None else workspace.numel()
+        if imp_mode != _lib.IMP_SOFTMAX_COLSUM and key_split:
+            # the room of this class's own parts (the launcher splits as far as the room allows)
+            ws_n = min(ws_n, _split_parts(plan, first, count, tile_rows, n_heads, cus) *
+                       n_row_idx * n_heads * _lib.ATTN_PART_FLOATS)
+        elif imp_mode != _lib.IMP_SOFTMAX_COLSUM:
+            ws_n = 0
         _lib.call("fdl_block_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                   q.shape[0], k_cache.shape[0], d_model, n_heads, d_model // n_heads,
                   plan.page_table_d.data_ptr(), plan.page_table.shape[0], plan.page_table.shape[1],
                   plan.page_log2, plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(),
                   n_row_idx, tile_rows, float(softmax_scale), out.data_ptr(), int(imp_mode),
-                  _ptr(imp_part), _ptr(workspace), 0 if workspace is None else workspace.numel(),
-                  stream)
+                  _ptr(imp_part), _ptr(workspace) if ws_n else None, ws_n, stream)
 
 
 def work_from_blocks(masked: torch.Tensor, tracked: torch.Tensor, n_seq: int, n_q_rows: int,

@@ -184,8 +184,9 @@ def test_build_work_tile_classes():
 
 def test_attention_workspace_sizes():
     """Key-split workspace: a class whose tiles x heads fill at most a quarter of the
-    compute units gets min(8, CUs / (tiles x heads)) parts of ATTN_PART_FLOATS per row-index
-    entry and head, the 256-row class none; softmax-importance workspace only past
+    compute units gets min(8, CUs / (tiles x heads), its largest tile's key blocks) parts of
+    ATTN_PART_FLOATS per row-index entry and head if that is at least four, the 256-row
+    class none; softmax-importance workspace only past
     ATTN_ONCHIP_BLOCKS key blocks. The constants match the header's."""
     from fdl import ops
     from fdl.schedule import make_plan
@@ -194,8 +195,13 @@ def test_attention_workspace_sizes():
         m = re.search(rf"#define FDL_{name} (\d+)", hdr)
         assert m and int(m.group(1)) == getattr(lib, name), name
     one = make_plan([SeqRows(0, 384, np.arange(40), 0)], contiguous_page_table(1, 384))
-    assert ops.attention_split_floats(one, 32, 256) == 8 * 40 * 32 * lib.ATTN_PART_FLOATS
+    # 384 keys = 6 key blocks: 6 parts, not 8 (two would be empty)
+    assert ops.attention_split_floats(one, 32, 256) == 6 * 40 * 32 * lib.ATTN_PART_FLOATS
     assert ops.attention_split_floats(one, 32, 160) == 5 * 40 * 32 * lib.ATTN_PART_FLOATS
+    short = make_plan([SeqRows(0, 192, np.arange(40), 0)], contiguous_page_table(1, 192))
+    assert ops.attention_split_floats(short, 32, 256) == 0  # 3 key blocks: under four parts
+    big = make_plan([SeqRows(0, 1024, np.arange(40), 0)], contiguous_page_table(1, 1024))
+    assert ops.attention_split_floats(big, 32, 256) == 8 * 40 * 32 * lib.ATTN_PART_FLOATS
     assert ops.attention_split_floats(one, 32, 127) == 0  # 32 workgroups: over a quarter
     three = make_plan([SeqRows(b, 1024, np.arange(64 * b, 64 * b + 64), 0) for b in range(3)],
                       contiguous_page_table(3, 1024))
