@@ -1640,9 +1640,13 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
   args.scale_log2 = softmax_scale * kLog2e;
   // Key split: a launch of 64- or 128-row tiles whose (tile, head) grid fills at most a
   // quarter of the device (without softmax-colsum importance, which needs every key of a
-  // row) spreads each tile's key blocks over 4 to kMaxKvParts workgroups when the workspace
-  // holds their partial rows, then merges them (two parts on a half-filled device cost more
-  // than they save).
+  // row) spreads each tile's key blocks over up to min(kMaxKvParts, CUs / grid) workgroups
+  // (at least four fit; two parts on a half-filled device cost more than they save), as
+  // many as the workspace holds partial rows for, then merges them. A caller that knows
+  // the tiles' block counts gives room for no more parts than blocks, with the same result
+  // bits: part z of p takes blocks [z nb / p, (z + 1) nb / p), so with p >= nb every
+  // non-empty part is one block, empty parts merge as exact zeros, and one part is the
+  // unsplit launch.
   int parts = 1;
   if (imp_mode != FDL_IMP_SOFTMAX_COLSUM && (tile_rows == 64 || tile_rows == 128) &&
       workspace != nullptr) {
@@ -1650,7 +1654,7 @@ int block_attention_launch(const char* fn, const void* q, const void* k_cache, c
     if (4 * grid <= cus) {
       const int64_t room = workspace_floats / (n_row_idx * n_heads * kPartFloats);
       const int64_t p = std::min<int64_t>({kMaxKvParts, cus / grid, room});
-      if (p >= 4) parts = static_cast<int>(p);
+      if (p >= 2) parts = static_cast<int>(p);
     }
   }
   if (parts > 1) {

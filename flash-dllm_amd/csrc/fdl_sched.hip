@@ -39,11 +39,12 @@ __device__ __forceinline__ int32_t* seq_of(const fdl_sched& s, int j) {
   return s.seq + FDL_SCHED_SEQ_FIELDS * j;
 }
 
-// Row i of the pass-1 confidences ranks before row k in the stable descending sort
-// (generate.py:230, :343; numpy's argsort of -conf, kind="stable", puts NaN last).
+// Row k of the pass-1 confidences ranks before row i in the descending sort
+// (generate.py:230, :343: x0_p.sort(descending=True), which puts NaN first, as the largest
+// value); ties in row order.
 __device__ __forceinline__ bool conf_before(double ck, int k, double ci, int i) {
   const bool nk = ck != ck, ni = ci != ci;
-  if (nk != ni) return ni;                 // a number before a NaN
+  if (nk != ni) return nk;                 // a NaN before a number
   if (nk || ck == ci) return k < i;        // equal (or both NaN): lower row first
   return ck > ci;
 }
@@ -430,7 +431,14 @@ __global__ __launch_bounds__(kSchedThreads) void sched_pack_kernel(fdl_sched s) 
 // keys: the attention and importance kernels skip them). The same grouping and tile
 // classes as fdl.schedule.build_work, without the host: tiles stay in group order within a
 // class instead of longest first.
-constexpr int kWfbMaxEntries = 1024;
+//
+// The tables pass through LDS in chunks of kWfbChunk entries, twice: the first pass finds
+// the groups and their row counts, the second gives each entry its first row (one cursor
+// per group for its masked rows and one for its tracked rows) and writes its row list. Only
+// the groups stay in LDS, so the table length is not bounded: a full recompute of 32
+// sequences at block_m 16 (generate.py:129-134) has about 1,800-2,800 entries.
+constexpr int kWfbChunk = 1024;
+constexpr int kWfbMaxGroups = 1024;
 constexpr int kWfbMaxSeq = 1024;
 
 struct WfbArgs {
@@ -445,93 +453,133 @@ struct WfbArgs {
 };
 
 __global__ __launch_bounds__(kSchedThreads) void work_from_blocks_kernel(WfbArgs a) {
-  __shared__ int s_gid_of_b[kWfbMaxSeq];                      // first group of a batch row
-  __shared__ int s_gb[kWfbMaxEntries], s_gk[kWfbMaxEntries];  // group key (batch, k_end)
-  __shared__ int s_gm[kWfbMaxEntries], s_gt[kWfbMaxEntries];  // its masked / tracked rows
-  __shared__ int s_goff[kWfbMaxEntries], s_cur[kWfbMaxEntries];  // first row; a cursor
-  __shared__ int s_eg[kWfbMaxEntries], s_eoff[kWfbMaxEntries];   // entry: group, first row
-  __shared__ int4 s_e[kWfbMaxEntries];  // the entries (b, k_end, q0, q1); b = -1: dropped
+  __shared__ int s_ghead[kWfbMaxSeq];                       // newest group of a batch row
+  __shared__ int s_gnext[kWfbMaxGroups];                    // next group of the same row
+  __shared__ int s_gb[kWfbMaxGroups], s_gk[kWfbMaxGroups];  // group key (batch, k_end)
+  __shared__ int s_gm[kWfbMaxGroups], s_gt[kWfbMaxGroups];  // its masked / tracked rows
+  __shared__ int s_goff[kWfbMaxGroups];                     // its first row
+  __shared__ int s_cm[kWfbMaxGroups], s_ct[kWfbMaxGroups];  // next masked / tracked row
+  __shared__ int4 s_e[kWfbChunk];   // a chunk of entries (b, k_end, q0, q1); b = -1: dropped
+  __shared__ int s_eoff[kWfbChunk];  // an entry's first row (-1: no rows written)
+  __shared__ int s_n_groups, s_err;
   __shared__ int s_used[3];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int n = a.n_masked + a.n_tracked;
-  for (int i = tid; i < a.n_seq; i += kSchedThreads) s_gid_of_b[i] = -1;
-  // stage the tables (an entry outside the tables' ranges is dropped)
-  for (int i = tid; i < n; i += kSchedThreads) {
-    const int64_t* src = i < a.n_masked ? a.masked + 4 * int64_t(i)
-                                        : a.tracked + 4 * int64_t(i - a.n_masked);
-    const int64_t b = src[0], k = src[1], q0 = src[2], q1 = src[3];
-    const bool ok = b >= 0 && b < a.n_seq && k > 0 && k <= a.max_k && q0 >= 0 && q1 >= q0 &&
-                    q1 <= a.n_q_rows;
-    s_e[i] = ok ? make_int4(int(b), int(k), int(q0), int(q1)) : make_int4(-1, 0, 0, 0);
+  const int max_rows = int(a.n_q_rows);  // < 2^31 (checked by the launcher)
+  for (int i = tid; i < a.n_seq; i += kSchedThreads) s_ghead[i] = -1;
+  if (tid == 0) {
+    s_n_groups = 0;
+    s_err = 0;
+  }
+  // entries [c0, c0 + cnt) into s_e (an entry outside the tables' ranges is dropped)
+  auto stage = [&](int c0, int cnt) {
+    for (int i = tid; i < cnt; i += kSchedThreads) {
+      const int e = c0 + i;
+      const int64_t* src = e < a.n_masked ? a.masked + 4 * int64_t(e)
+                                          : a.tracked + 4 * int64_t(e - a.n_masked);
+      const int64_t b = src[0], k = src[1], q0 = src[2], q1 = src[3];
+      const bool ok = b >= 0 && b < a.n_seq && k > 0 && k <= a.max_k && q0 >= 0 && q1 >= q0 &&
+                      q1 <= a.n_q_rows;
+      s_e[i] = ok ? make_int4(int(b), int(k), int(q0), int(q1)) : make_int4(-1, 0, 0, 0);
+    }
+  };
+  auto lookup = [&](int b, int k) {
+    int g = s_ghead[b];
+    while (g >= 0 && s_gk[g] != k) g = s_gnext[g];
+    return g;
+  };
+  __syncthreads();
+  // pass 1: groups in order of first appearance, with their masked and tracked row counts
+  // (saturated past max_rows: such a group gets no tile)
+  for (int c0 = 0; c0 < n; c0 += kWfbChunk) {
+    const int cnt = min(kWfbChunk, n - c0);
+    stage(c0, cnt);
+    __syncthreads();
+    if (tid == 0) {
+      int G = s_n_groups, err = s_err;
+      for (int i = 0; i < cnt; ++i) {
+        const int4 e = s_e[i];
+        if (e.x < 0) {
+          err |= 1;
+          continue;
+        }
+        int g = lookup(e.x, e.y);
+        if (g < 0) {
+          if (G == kWfbMaxGroups) {
+            err |= 16;
+            continue;
+          }
+          g = G++;
+          s_gb[g] = e.x;
+          s_gk[g] = e.y;
+          s_gm[g] = s_gt[g] = 0;
+          s_gnext[g] = s_ghead[e.x];
+          s_ghead[e.x] = g;
+        }
+        int& c = c0 + i < a.n_masked ? s_gm[g] : s_gt[g];
+        c = int(min(int64_t(c) + (e.w - e.z), int64_t(max_rows) + 1));
+      }
+      s_n_groups = G;
+      s_err = err;
+    }
+    __syncthreads();
+  }
+  const int G = s_n_groups;
+  if (tid == 0) {
+    int64_t off = 0;
+    for (int g = 0; g < G; ++g) {
+      const int o = int(min(off, int64_t(max_rows)));
+      s_goff[g] = s_cm[g] = o;
+      s_ct[g] = int(min(off + s_gm[g], int64_t(max_rows)));
+      off += int64_t(s_gm[g]) + s_gt[g];
+    }
+    if (off > max_rows) s_err |= 2;
   }
   __syncthreads();
-  auto entry = [&](int i, int64_t (&e)[4]) {
-    const int4 v = s_e[i];
-    e[0] = v.x;
-    e[1] = v.y;
-    e[2] = v.z;
-    e[3] = v.w;
-  };
-  if (tid == 0) {
-    int err = 0, G = 0;
-    // groups in order of first appearance, with their masked and tracked row counts
-    for (int i = 0; i < n; ++i) {
-      int64_t e[4];
-      entry(i, e);
-      s_eg[i] = -1;
-      if (e[0] < 0) {
-        err |= 1;
-        continue;
-      }
-      const int b = int(e[0]), k = int(e[1]);
-      int g = s_gid_of_b[b];
-      if (g < 0 || s_gk[g] != k) {  // a new key, or a batch row under a second key count
-        int f = -1;
-        for (int j = 0; j < G && f < 0; ++j)
-          if (s_gb[j] == b && s_gk[j] == k) f = j;
-        if (f < 0) {
-          f = G++;
-          s_gb[f] = b;
-          s_gk[f] = k;
-          s_gm[f] = s_gt[f] = 0;
-          if (s_gid_of_b[b] < 0) s_gid_of_b[b] = f;
-        }
-        g = f;
-      }
-      s_eg[i] = g;
-      if (i < a.n_masked)
-        s_gm[g] += int(e[3] - e[2]);
-      else
-        s_gt[g] += int(e[3] - e[2]);
-    }
-    int off = 0;
-    for (int g = 0; g < G; ++g) {
-      s_goff[g] = off;
-      off += s_gm[g] + s_gt[g];
-    }
-    if (off > a.n_q_rows) err |= 2;
-    // first row of every entry: a group's masked entries in order, then its tracked ones
-    for (int kind = 0; kind < 2; ++kind) {
-      for (int g = 0; g < G; ++g) s_cur[g] = s_goff[g] + (kind ? s_gm[g] : 0);
-      for (int i = kind ? a.n_masked : 0; i < (kind ? n : a.n_masked); ++i) {
-        const int g = s_eg[i];
+  // pass 2: each entry's first row (a group's masked entries in order, then its tracked
+  // ones; an entry whose rows would pass max_rows gets none) and its row list q0 .. q1 - 1
+  for (int c0 = 0; c0 < n; c0 += kWfbChunk) {
+    const int cnt = min(kWfbChunk, n - c0);
+    stage(c0, cnt);
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 0; i < cnt; ++i) {
+        const int4 e = s_e[i];
+        const int g = e.x < 0 ? -1 : lookup(e.x, e.y);
+        s_eoff[i] = -1;
         if (g < 0) continue;
-        int64_t e[4];
-        entry(i, e);
-        s_eoff[i] = s_cur[g];
-        s_cur[g] += int(e[3] - e[2]);
+        int& cur = c0 + i < a.n_masked ? s_cm[g] : s_ct[g];
+        if (e.w - e.z > max_rows - cur) continue;  // the group is past max_rows: no tile
+        s_eoff[i] = cur;
+        cur += e.w - e.z;
       }
     }
+    __syncthreads();
+    for (int i = wave; i < cnt; i += kSchedWaves) {
+      const int o = s_eoff[i];
+      if (o < 0) continue;
+      const int4 e = s_e[i];
+      for (int r = lane; r < e.w - e.z; r += kWave) a.row_idx[o + r] = int32_t(e.z + r);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int err = s_err;
     // tiles, in group order within each class
     int nl = 0, nm = 0, ns = 0;
     for (int g = 0; g < G; ++g) {
-      const int rows = s_gm[g] + s_gt[g], start = s_goff[g], n_imp = s_gm[g];
+      const int64_t rows64 = int64_t(s_gm[g]) + s_gt[g];
+      if (rows64 == 0) continue;
+      if (s_goff[g] + rows64 > max_rows) {  // rows past max_rows were not written
+        err |= 2;
+        continue;
+      }
+      const int rows = int(rows64), start = s_goff[g], n_imp = s_gm[g];
       auto put = [&](int slot, int r0, int nr, int imp) {
         u32x4* w = reinterpret_cast<u32x4*>(a.work + 8 * int64_t(slot));
         w[0] = u32x4{uint32_t(s_gb[g]), 0u, uint32_t(s_gk[g]), uint32_t(r0)};
         w[1] = u32x4{uint32_t(nr), uint32_t(imp), 0u, 0u};
       };
-      if (rows == 0) continue;
       if (rows <= 64) {
         if (ns < a.cap_short) put(a.cap_long + a.cap_mid + ns, start, rows, n_imp);
         else err |= 4;
@@ -567,15 +615,6 @@ __global__ __launch_bounds__(kSchedThreads) void work_from_blocks_kernel(WfbArgs
       w[0] = u32x4{0u, 0u, 0u, 0u};
       w[1] = u32x4{0u, 0u, 0u, 0u};
     }
-  // row lists: entry i's rows q0 .. q1 - 1 from its first row
-  for (int i = 0; i < n; ++i) {
-    if (s_eg[i] < 0) continue;
-    int64_t e[4];
-    entry(i, e);
-    const int rows = int(e[3] - e[2]), o = s_eoff[i];
-    for (int r = tid; r < rows; r += kSchedThreads)
-      if (o + r < a.n_q_rows) a.row_idx[o + r] = int32_t(e[2] + r);
-  }
 }
 
 int check_sched(const char* fn, const fdl_sched* s) {
@@ -642,9 +681,9 @@ extern "C" int fdl_work_from_blocks(const int64_t* masked, int64_t n_masked, con
                                     int64_t cap_mid, int64_t cap_short, int32_t* row_idx,
                                     int32_t* status, void* stream) {
   using namespace fdl;
-  FDL_REQUIRE(n_masked >= 0 && n_tracked >= 0 && n_masked + n_tracked <= kWfbMaxEntries,
-              FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks: %lld table rows (at most %d)",
-              (long long)(n_masked + n_tracked), kWfbMaxEntries);
+  FDL_REQUIRE(n_masked >= 0 && n_tracked >= 0 && n_masked + n_tracked < (int64_t(1) << 30),
+              FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks: %lld table rows (fewer than 2^30)",
+              (long long)(n_masked + n_tracked));
   FDL_REQUIRE(n_seq >= 1 && n_seq <= kWfbMaxSeq, FDL_ERR_UNSUPPORTED,
               "fdl_work_from_blocks: n_seq = %lld outside [1, %d]", (long long)n_seq, kWfbMaxSeq);
   FDL_REQUIRE(n_q_rows >= 0 && n_q_rows < (int64_t(1) << 31) && max_k >= 1 &&

@@ -69,6 +69,15 @@ def get_rotary_embedding(seq_len: int, dim: int, rope_theta: float, device) -> t
     return positions.sin().float(), positions.cos().float()
 
 
+def conf_order(conf: np.ndarray) -> np.ndarray:
+    """Row order of `x0_p.sort(descending=True)` (generate.py:230, :343): descending, NaN
+    before every number (torch sorts NaN as the largest value), ties in row order (the
+    reference's sort is not declared stable; this fixes its tie order)."""
+    conf = np.asarray(conf, dtype=np.float64)
+    nan = np.isnan(conf)
+    return np.lexsort((-np.where(nan, 0.0, conf), ~nan))
+
+
 def make_blocks(j: int, seqlen_k, start_m: int, end_m: int, block_m: int) -> np.ndarray:
     """(batch, k_end, q_start, q_end) rows over [start_m, end_m) (llada/generate.py:52-58)."""
     starts = np.arange(start_m, end_m, block_m, dtype=np.int64)
@@ -470,7 +479,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     length_num = len(s.masked) - int(lmask.sum())
                 else:
                     length_num = len(s.masked)
-                order = np.argsort(-conf, kind="stable")
+                order = conf_order(conf)
                 keep = max(int((conf >= threshold).sum()), 1)
                 x_draft[s.masked] = toks
                 full_pos[j, s.nd:s.nd + len(s.masked)] = s.masked[order]
@@ -575,7 +584,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                 toks = x0_all[rows]
                 if s.decoded_eos != -1:
                     conf[s.masked >= s.predicted_length] = 0
-                order = np.argsort(-conf, kind="stable")
+                order = conf_order(conf)
                 keep = max(int((conf[order] >= threshold).sum()), 1)
                 full_pos[j, s.nd:s.nd + nm] = s.masked[order]
                 new_pos = full_pos[j, s.nd:s.nd + keep].copy()

@@ -96,20 +96,19 @@ def _class_ranges(plan: AttnPlan):
 
 
 def attention_workspace_floats(plan: AttnPlan, n_heads: int) -> int:
-    """fp32 workspace that lets every importance tile of the plan keep its softmax-importance
-    probabilities for one pass (fdl_block_attention's workspace; the launches of one call
-    reuse it). Tiles of at most ATTN_ONCHIP_BLOCKS key blocks keep them on chip: a plan
-    without longer importance tiles needs none."""
-    need = 0
-    for first, count, _ in _class_ranges(plan):
-        if count == 0:
-            continue
-        w = plan.work[first:first + count]
-        blocks = int(((w[:, 2] - w[:, 1] + 63) // 64).max()) if (w[:, 5] > 0).any() else 0
-        if blocks <= _lib.ATTN_ONCHIP_BLOCKS:
-            continue
-        need = max(need, count * n_heads * blocks * _lib.ATTN_WS_FLOATS_PER_BLOCK)
-    return need
+    """fp32 workspace that lets every importance tile of the plan's 64-row class keep its
+    softmax-importance probabilities for one pass (fdl_block_attention's workspace; the
+    launches of one call reuse it). Only 64-row tiles keep them: the 128-row and 256-row
+    kernels take a second pass over K instead. Tiles of at most ATTN_ONCHIP_BLOCKS key blocks
+    keep them on chip: a plan without longer 64-row importance tiles needs none."""
+    first, count, _ = _class_ranges(plan)[2]
+    w = plan.work[first:first + count]
+    if count == 0 or w.shape[0] != count or not (w[:, 5] > 0).any():
+        return 0
+    blocks = int(((w[:, 2].astype(np.int64) - w[:, 1] + 63) // 64).max())
+    if blocks <= _lib.ATTN_ONCHIP_BLOCKS:
+        return 0
+    return count * n_heads * blocks * _lib.ATTN_WS_FLOATS_PER_BLOCK
 
 
 _cu_count: dict = {}
@@ -125,19 +124,22 @@ def _cus(dev: torch.device) -> int:
 def _split_parts(plan: AttnPlan, first: int, count: int, tile_rows: int, n_heads: int,
                  cus: int) -> int:
     """Key-split parts of one tile class (0: none): a class of 64- or 128-row tiles whose
-    count * n_heads workgroups fill at most a quarter of the `cus` compute units spreads each
-    tile's key blocks over min(ATTN_MAX_KV_PARTS, cus // (count * n_heads), its largest
-    tile's block count) workgroups, if that is at least four (fewer cost more than they
-    save; more than the blocks would leave parts empty). A plan built on the device has no
-    host copy of its tiles: no block cap then."""
+    count * n_heads workgroups fill at most a quarter of the `cus` compute units (so that at
+    least four parts fit; two parts on a half-filled device cost more than they save)
+    spreads each tile's key blocks over min(ATTN_MAX_KV_PARTS, cus // (count * n_heads))
+    workgroups, capped at its largest tile's block count (more parts would stay empty).
+
+    The cap changes no result bit: part z of p takes blocks [z nb / p, (z + 1) nb / p), so
+    with p >= nb every non-empty part holds one block, in the same order, and empty parts
+    add exact zeros in the merge; one part is the unsplit launch. A plan built on the device
+    has no host copy of its tiles, so it runs uncapped with the same results."""
     if count == 0 or tile_rows == LONG_TILE_ROWS or 4 * count * n_heads > cus:
         return 0
+    parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads))
     w = plan.work[first:first + count]
-    blocks = _lib.ATTN_MAX_KV_PARTS
     if w.shape[0] == count:
-        blocks = int(((w[:, 2].astype(np.int64) - w[:, 1] + 63) // 64).max())
-    parts = min(_lib.ATTN_MAX_KV_PARTS, cus // (count * n_heads), blocks)
-    return parts if parts >= 4 else 0
+        parts = min(parts, int(((w[:, 2].astype(np.int64) - w[:, 1] + 63) // 64).max()))
+    return parts if parts >= 2 else 0
 
 
 def attention_split_floats(plan: AttnPlan, n_heads: int, cus: int) -> int:

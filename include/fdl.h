@@ -123,8 +123,12 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
  *            quarter of the device's compute units splits every tile's key blocks over
  *            p = min(FDL_ATTN_MAX_KV_PARTS, CUs / (n_work * n_heads)) workgroups when the
  *            workspace holds p * n_row_idx * n_heads * FDL_ATTN_PART_FLOATS floats (fewer
- *            parts when it holds less, none below 4 or without a workspace), and merges their partial rows
- *            in a second kernel: same attention within rounding, raw importance unchanged.
+ *            parts when it holds less, none below 2, below 4 device-filling parts or without
+ *            a workspace), and merges their partial rows in a second kernel: same attention
+ *            within rounding, raw importance unchanged. Room for fewer than p parts but at
+ *            least as many as the longest tile's 64-key blocks gives the same bits as room
+ *            for p (part z of p takes blocks [z nb / p, (z + 1) nb / p): one block per
+ *            non-empty part either way).
  *            Contents need no initialisation and are left undefined.
  */
 #define FDL_ATTN_WS_FLOATS_PER_BLOCK (32 * 64 + 32)
@@ -397,19 +401,22 @@ int fdl_sched_pack(const fdl_sched* state, void* stream);
  * tables (rows (batch, k_end, q0, q1), generate.py:52-58, :146-163, :439-465; launched at
  * flash_cache_triton.py:561-607); this builds the work items and row list that
  * fdl_block_attention takes from them.
- *   masked, tracked int64 [n][4] (device), n_masked + n_tracked <= 1024
+ *   masked, tracked int64 [n][4] (device), any number of entries (n_masked + n_tracked
+ *   < 2^30; the tables pass through the workgroup's LDS in chunks of 1024 entries)
  *   rows of a (batch, k_end) pair are grouped in order of first appearance: its masked rows
- *   (the importance rows) then its tracked rows; at most n_seq such pairs (the reference
+ *   (the importance rows) then its tracked rows; at most 1024 such pairs (the reference
  *   has one k_end per batch row). A group of up to 64 rows is one 64-row tile, up to 128 one
- *   128-row tile, more one 256-row tile per 256 rows.
+ *   128-row tile, more one 256-row tile per 256 rows. n_seq <= 1024.
  *   work int32 [cap_long + cap_mid + cap_short][8], 16-byte aligned: the 256-row tiles from
  *   item 0, the 128-row tiles from item cap_long, the 64-row tiles from cap_long + cap_mid;
  *   unused items are zero (no rows, no keys), which fdl_block_attention and
  *   fdl_importance_accumulate skip, so each region can be launched whole. cap_long =
  *   n_q_rows / 128 and cap_mid = cap_short = n_seq always suffice.
  *   row_idx int32 [n_q_rows]; status int32 [4] (16-byte aligned) or NULL: tiles of each
- *   class and error flags (1: an entry out of range, dropped; 2: more rows than n_q_rows;
- *   4: a region over capacity; 8: more than 256 importance rows in a group).
+ *   class and error flags (1: an entry out of range, dropped; 2: more rows than n_q_rows,
+ *   the groups past n_q_rows get no tiles; 4: a region over capacity; 8: more than 256
+ *   importance rows in a group; 16: more than 1024 (batch, k_end) groups, the entries of
+ *   the further groups dropped).
  * One workgroup; enqueued on `stream`.
  */
 int fdl_work_from_blocks(const int64_t* masked, int64_t n_masked, const int64_t* tracked,

@@ -5,7 +5,7 @@ TEST INFRASTRUCTURE ONLY: the oracle that the product scheduler
 follows the reference's control flow and tensor bookkeeping one statement group at a time
 (device tensors, per-sequence Python loops); the only decisions it fixes that the
 reference leaves open are the two sort tie rules:
-  * confidence sort (:230, :343): stable, ties keep row order;
+  * confidence sort (:230, :343): ties keep row order (NaN first, as torch sorts it);
   * importance sort (:365): ascending by score, ties put the higher slot first (so the
     highest-ranked tail prefers lower slots).
 It calls `model(x_query, use_cache=True, lengths=..., positions=...)` exactly like the
@@ -50,7 +50,11 @@ def _rope(seq_len, dim, theta, device):
 
 
 def _stable_desc(v: torch.Tensor) -> torch.Tensor:
-    return torch.from_numpy(np.argsort(-v.cpu().numpy(), kind="stable")).to(v.device)
+    """`v.sort(descending=True)` order (generate.py:230, :343): NaN first, as torch sorts it,
+    then descending; ties in row order."""
+    a = v.cpu().numpy().astype(np.float64)
+    nan = np.isnan(a)
+    return torch.from_numpy(np.lexsort((-np.where(nan, 0.0, a), ~nan))).to(v.device)
 
 
 def _importance_asc(scores: torch.Tensor, slots: torch.Tensor) -> torch.Tensor:

@@ -107,8 +107,8 @@ def test_launchers_reject_bad_scalars_without_gpu():
     st.q_cap = -1
     _expect(lib.FDL_ERR_SHAPE, "fdl_sched_pack", ctypes.byref(st), None)
     # device work list from block tables: too many entries, no sequences, NULL tables
-    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks", None, 1000, None, 25, 8, 64, 1024,
-            None, 0, 8, 8, None, None, None)
+    _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks", None, 1 << 29, None, 1 << 29, 8, 64,
+            1024, None, 0, 8, 8, None, None, None)
     _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_work_from_blocks", None, 1, None, 1, 0, 64, 1024, None,
             0, 8, 8, None, None, None)
     _expect(lib.FDL_ERR_NULL, "fdl_work_from_blocks", None, 1, None, 1, 8, 64, 1024, None, 0, 8,
@@ -199,7 +199,10 @@ def test_attention_workspace_sizes():
     assert ops.attention_split_floats(one, 32, 256) == 6 * 40 * 32 * lib.ATTN_PART_FLOATS
     assert ops.attention_split_floats(one, 32, 160) == 5 * 40 * 32 * lib.ATTN_PART_FLOATS
     short = make_plan([SeqRows(0, 192, np.arange(40), 0)], contiguous_page_table(1, 192))
-    assert ops.attention_split_floats(short, 32, 256) == 0  # 3 key blocks: under four parts
+    # 3 key blocks: 3 parts, the same bits as the 8 of a plan built on the device
+    assert ops.attention_split_floats(short, 32, 256) == 3 * 40 * 32 * lib.ATTN_PART_FLOATS
+    tiny = make_plan([SeqRows(0, 64, np.arange(40), 0)], contiguous_page_table(1, 64))
+    assert ops.attention_split_floats(tiny, 32, 256) == 0  # one key block: one part, no split
     big = make_plan([SeqRows(0, 1024, np.arange(40), 0)], contiguous_page_table(1, 1024))
     assert ops.attention_split_floats(big, 32, 256) == 8 * 40 * 32 * lib.ATTN_PART_FLOATS
     assert ops.attention_split_floats(one, 32, 127) == 0  # 32 workgroups: over a quarter
@@ -213,6 +216,18 @@ def test_attention_workspace_sizes():
     assert ops.attention_workspace_floats(soft, 32) == 0  # 24 blocks: on chip
     soft = make_plan([SeqRows(0, 1600, np.arange(64), 32)], contiguous_page_table(1, 1600))
     assert ops.attention_workspace_floats(soft, 32) == 32 * 25 * lib.ATTN_WS_FLOATS_PER_BLOCK
+    # only the 64-row class keeps probabilities in the workspace: 128-row and 256-row tiles
+    # (8 full recomputes of 4096 keys, 32 heads) take a second pass over K and need none
+    pt = contiguous_page_table(8, 4096)
+    full = make_plan([SeqRows(b, 4096, np.arange(4096 * b, 4096 * b + 4096), 32) for b in range(8)], pt)
+    assert full.n_long == 128 and ops.attention_workspace_floats(full, 32) == 0
+    mid = make_plan([SeqRows(b, 4096, np.arange(100 * b, 100 * b + 100), 32) for b in range(8)], pt)
+    assert mid.n_mid == 8 and ops.attention_workspace_floats(mid, 32) == 0
+    # beside them, the 64-row tiles alone are counted (2 tiles x 32 heads x 30 blocks)
+    mixed = make_plan([SeqRows(0, 4096, np.arange(4096), 32), SeqRows(1, 4096, np.arange(4096, 4196), 32),
+                       SeqRows(2, 1920, np.arange(4196, 4260), 32), SeqRows(3, 1600, np.arange(4260, 4300), 8)],
+                      pt)
+    assert ops.attention_workspace_floats(mixed, 32) == 2 * 32 * 30 * lib.ATTN_WS_FLOATS_PER_BLOCK
 
 
 def test_validate_work():

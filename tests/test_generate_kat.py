@@ -155,6 +155,22 @@ def test_pass1_acceptance_ranking_and_eos_length_mask(impl):
 
 
 @pytest.mark.parametrize("impl", IMPLS)
+def test_pass1_nan_confidence_ranks_first(impl):
+    """x0_p.sort(descending=True) (generate.py:343) puts NaN first, as torch sorts it: with
+    no confidence at the threshold, keep = 1 takes the NaN row (slot 5), whose token is
+    torch.max's index for an all-NaN softmax row (0), and not the best number (slot 4)."""
+    script = {0: {"rows": {4: (1, 0.5), 5: (2, float("nan")), 6: (3, 0.3), 7: (4, 0.2)}}}
+    model = Scripted(script)
+    resp, _, _, _ = _run(impl, model, [P0], 1, **_kw())
+    c = model.calls
+    # after step 0: full_pos[4:8] = [5, 4, 6, 7], nd = 5; full_pos[:4] = 0..3 all at score 0
+    # -> higher slot first: [3, 2, 1, 0]; tracked = full_pos[1:5] = [2, 1, 0, 5]
+    assert c[1]["qpos"] == [4, 6, 7, 8] + [2, 1, 0, 5]
+    assert c[1]["x"] == [MASK] * 4 + [P0[2], P0[1], P0[0], 0]
+    assert resp[0][:2] == [3, 0]  # slot 4 by the default row at step 1, slot 5 the NaN row's
+
+
+@pytest.mark.parametrize("impl", IMPLS)
 @pytest.mark.parametrize("track,mask_num,tracked", [
     (1, 1, [2, 0, 5, 7]),                                   # last bm decoded entries
     (2, 1, [1, 3, 2, 0, 5, 7]),                             # 2 bm entries, clipped at 0

@@ -43,13 +43,21 @@ def _forward_both(model, x_ids, positions_fn, lengths):
     return out_h, out_t, kv_h, kv_t, sc_h, sc_t
 
 
-def test_driver_matches_torch_driver_prefill_and_step():
+@pytest.mark.parametrize("B,bm,pl,gen", [
+    (2, 32, 96, 64),
+    # the reference's evaluation preset (llada/eval_gsm8k.sh:7-15: batch 32, block 16, gen
+    # 512) at a 1408-key cache: step 0 tracks every slot (generate.py:129-134), so the
+    # tables hold 32 x 88 = 2816 entries, built into the work list on the GPU
+    (32, 16, 800, 512),
+])
+def test_driver_matches_torch_driver_prefill_and_step(B, bm, pl, gen):
     """Step 0 (every slot recomputed) then a steady-state step (masked + tracked rows),
-    through all layers: logits, caches and importance scores agree."""
+    through all layers, with the reference's calling convention (info = [], int64 block
+    tables on the GPU; generate.py:192-198): logits, caches and importance scores agree
+    with the unfused torch driver."""
     torch.manual_seed(0)
     model = _model()
     cfg = model.config
-    B, bm, pl, gen = 2, 32, 96, 64
     L = orc.max_length_for([pl], gen, bm)
     k_end = orc.seqlen_k_for(pl, gen)
     sin, cos = get_rotary_embedding(L, 128, cfg.rope_theta, DEV)
@@ -73,6 +81,8 @@ def test_driver_matches_torch_driver_prefill_and_step():
         mb_t = torch.from_numpy(np.concatenate(mb)).to(DEV)
         tb_t = torch.from_numpy(np.concatenate(tb)).to(DEV)
         qp = torch.from_numpy(np.concatenate(qpos)).to(DEV)
+        print(f"B={B} bm={bm} k_end={k_end}: {len(mb_t) + len(tb_t)} table entries, {acc} rows",
+              flush=True)
         lengths = [[-1] * B, None, mb_t, tb_t, torch.cat([mb_t, tb_t]), list(range(B)), len(mb_t), L,
                    bm, 128, None, False]
 
@@ -89,18 +99,81 @@ def test_driver_matches_torch_driver_prefill_and_step():
     for (kh, vh), (kt, vt) in zip(kv_h, kv_t):
         np.testing.assert_allclose(kh.float().cpu().numpy(), kt.float().cpu().numpy(), atol=3e-2, rtol=2e-2)
         np.testing.assert_allclose(vh.float().cpu().numpy(), vt.float().cpu().numpy(), atol=3e-2, rtol=2e-2)
-    # the raw-logit scores of layer 2 sum q.k over its 32 masked rows and 4 heads; the two
+    # the raw-logit scores of layer 2 sum q.k over its bm masked rows and 4 heads; the two
     # drivers feed layer 2 hidden states rounded differently (one bf16 rounding of the block's
     # residual add here, two in the unfused modules), so the scores differ by a few bf16 ulps
     # of q.k. The importance arithmetic itself is checked against float64 on the same Q and
     # K to 4e-6 (tests/test_gpu_topk_parity.py).
     np.testing.assert_allclose(sc_h.cpu().numpy(), sc_t.cpu().numpy(), atol=4e-2, rtol=2e-2)
-    # steady state: 32 masked + 32 tracked random decoded slots per sequence
-    masked = [np.arange(pl + 32, pl + 64)] * B
-    tracked = [np.sort(rng.choice(pl + 32, 32, replace=False)) for _ in range(B)]
+    # steady state: bm masked + bm tracked random decoded slots per sequence
+    masked = [np.arange(pl + bm, pl + 2 * bm)] * B
+    tracked = [np.sort(rng.choice(pl + bm, bm, replace=False)) for _ in range(B)]
     out_h, out_t, kv_h, kv_t, sc_h, sc_t = run(masked, tracked)
     np.testing.assert_allclose(out_h.cpu().numpy(), out_t.cpu().numpy(), atol=5e-2, rtol=5e-2)
+    for (kh, vh), (kt, vt) in zip(kv_h, kv_t):
+        np.testing.assert_allclose(kh.float().cpu().numpy(), kt.float().cpu().numpy(), atol=3e-2, rtol=2e-2)
     np.testing.assert_allclose(sc_h.cpu().numpy(), sc_t.cpu().numpy(), atol=4e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("verify", [False, True])
+@pytest.mark.parametrize("bm", [16, 32])
+def test_reference_loop_through_hip_driver_matches_product_loop(verify, bm):
+    """The reference's decode loop, restated statement for statement
+    (oracle/generate_oracle.py: model(x_query, use_cache=True, lengths, positions) with
+    info = [], int64 block tables and the dense verify mask on the GPU; generate.py:192-198,
+    :299-301), driving the HIP drop-in driver (flash_cache_hip, imported at
+    modeling_llada.py:55), against the product loop (fdl.generate) on the same HIP kernels:
+    the same tokens, token counts and per-prompt step counts, with a refill (three prompts
+    in two batch rows). Peaked logits (LM-head std 1) make steps accept several tokens, and
+    gamma 0.5 lets Flash-Verify accept drafts.
+
+    EOS is set to tokens the model emits often (a probe decode picks them), so sequences
+    end early and the predicted-length masking runs. With some of them the reference loop
+    itself fails: a sequence that keeps one low-confidence position undecoded slides its
+    masked block into the EOS padding until the block is cut short by the slot row end, and
+    generate.py:215/:235 then index with a shorter block (a shape mismatch; the product
+    loop reads the short block as is). Such an EOS is skipped; two that complete must
+    match."""
+    from oracle.generate_oracle import generate_oracle
+    model = _model(lm_head_std=1.0, seed=5)
+    lengths = [70, 96, 64]
+    rng = np.random.default_rng(7)
+    prompts = [torch.from_numpy(rng.integers(0, 2040, n)) for n in lengths]
+    kw = dict(gen_length=48, block_length=bm, mask_id=2046, threshold=0.9, gamma=0.5,
+              track_num=1, mask_num=1, verify=verify)
+    probe, _, _ = generate_with_Flash_dLLM(model, prompts, lengths, 2, [None] * 3, [0] * 3,
+                                           eos_id=2045, use_gpu_rank=False, rows_only=False, **kw)
+    counts = np.bincount(np.concatenate([np.asarray(r) for r in probe]))
+    matched, accepted = 0, 0
+    for eos in np.argsort(-counts, kind="stable")[:8]:
+        eos = int(eos)
+        steps_o = [0] * 3
+        try:
+            resp_o, nt_o, mx_o = generate_oracle(model, prompts, lengths, 2, steps_o, eos_id=eos,
+                                                 **kw)
+        except RuntimeError as e:
+            if "shape mismatch" not in str(e):
+                raise
+            print(f"eos {eos}: the reference loop fails (masked block cut short)", flush=True)
+            continue
+        steps_p = [0] * 3
+        stats = DecodeStats()
+        resp_p, nt_p, mx_p = generate_with_Flash_dLLM(model, prompts, lengths, 2, [None] * 3,
+                                                      steps_p, eos_id=eos, use_gpu_rank=False,
+                                                      rows_only=False, stats=stats, **kw)
+        print(f"verify={verify} bm={bm} eos={eos}: steps {steps_o} / {steps_p}, tokens {nt_o} / "
+              f"{nt_p}, verify accepted {stats.verify_accepted}", flush=True)
+        assert steps_p == steps_o and (nt_p, mx_p) == (nt_o, mx_o)
+        for i in range(3):
+            assert resp_p[i] == resp_o[i], f"eos {eos}, prompt {i}"
+        assert max(steps_o) > 1
+        matched += 1
+        accepted += stats.verify_accepted
+        if matched == 2:
+            break
+    assert matched == 2
+    if verify:
+        assert accepted > 0
 
 
 def _fp32_twin(model):

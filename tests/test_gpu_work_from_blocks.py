@@ -46,19 +46,26 @@ def _tiles(work, row_idx, first, count):
     return sorted(out)
 
 
+# per case: per sequence (k_end, masked rows, tracked rows), block_m
 CASES = {
-    "decode": [(768, 32, 32)] * 8,
-    "mixed": [(768, 32, 32), (512, 32, 64), (1024, 32, 0), (640, 0, 48), (900, 32, 600),
-              (1500, 32, 1468), (384, 32, 8), (256, 0, 256)],
-    "full_recompute": [(1024, 32, 992)] * 4,
+    "decode": ([(768, 32, 32)] * 8, 32),
+    "mixed": ([(768, 32, 32), (512, 32, 64), (1024, 32, 0), (640, 0, 48), (900, 32, 600),
+               (1500, 32, 1468), (384, 32, 8), (256, 0, 256)], 32),
+    "full_recompute": ([(1024, 32, 992)] * 4, 32),
+    # the reference's evaluation preset (batch 32, block 16; llada/eval_gsm8k.sh:7-15): at
+    # step 0 every slot is tracked (generate.py:129-134): 32 x 88 = 2816 table entries,
+    # passing through the builder's LDS in three chunks
+    "eval_preset_step0": ([(1408, 16, 1392)] * 32, 16),
+    "eval_preset_steady": ([(1408, 16, 16 + 16 * (j % 3)) for j in range(32)], 16),
 }
 
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_device_work_list_matches_host_builder(case):
-    rows = CASES[case]
+    rows, bm = CASES[case]
     B, L = len(rows), 1536
-    mb, tb, Q = _tables(rows)
+    mb, tb, Q = _tables(rows, bm)
+    print(f"{case}: {len(mb) + len(tb)} table entries, {Q} rows", flush=True)
     table = contiguous_page_table(B, L)
     table_d = torch.from_numpy(table).to(DEV)
     status = torch.zeros(4, dtype=torch.int32, device=DEV)

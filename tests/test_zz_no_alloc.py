@@ -60,8 +60,13 @@ def _run_both(case, imp_mode):
     sc_new = scores0.clone()
     imp = torch.zeros((H, n_slots), dtype=torch.float32, device=DEV)
     # the workspace entry point keeps the softmax probabilities for one pass as the
-    # scratch of the allocation-free one does for these sizes
-    ws = torch.empty(max(ops.attention_workspace_floats(plan, H), 4), dtype=torch.float32, device=DEV)
+    # scratch of the allocation-free one does for these sizes; in the other modes neither
+    # leg gets a workspace (one would let fdl_block_attention split the keys of a launch
+    # that fills at most a quarter of the device, which the allocation-free entry never does)
+    ws = None
+    if imp_mode == lib.IMP_SOFTMAX_COLSUM:
+        ws = torch.empty(max(ops.attention_workspace_floats(plan, H), 4), dtype=torch.float32,
+                         device=DEV)
     n_idx = max(int(plan.row_idx.size), 1)
     for first, count, tile_rows in _classes(plan):
         if count == 0:
@@ -71,7 +76,8 @@ def _run_both(case, imp_mode):
                   plan.page_log2, plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(),
                   n_idx, tile_rows, scale)
         lib.call("fdl_block_attention", q.data_ptr(), *common, out_ref.data_ptr(), imp_mode,
-                 imp.data_ptr() if imp_mode else None, ws.data_ptr(), ws.numel(), stream)
+                 imp.data_ptr() if imp_mode else None, None if ws is None else ws.data_ptr(),
+                 0 if ws is None else ws.numel(), stream)
         if imp_mode:
             lib.call("fdl_importance_accumulate", imp.data_ptr(), H, n_slots,
                      plan.page_table_d.data_ptr(), plan.page_table.shape[0],
