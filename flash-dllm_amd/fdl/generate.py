@@ -48,8 +48,8 @@ import torch
 import torch.nn.functional as F
 
 from . import ops
-from .schedule import (DEFAULT_PAGE_LOG2, PagePool, SeqRows, contiguous_page_table, make_plan,
-                       page_slots)
+from .schedule import (DEFAULT_PAGE_LOG2, PagedRows, PagePool, SeqRows, contiguous_page_table,
+                       make_plan, pages_reserved)
 
 
 def get_rotary_embedding(seq_len: int, dim: int, rope_theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -114,6 +114,9 @@ class DecodeStats:
     wall_s: float = 0.0
     per_step_s: list = field(default_factory=list)
     per_step_decoded: list = field(default_factory=list)  # tokens decoded in each step
+    # host schedule: the token ids x[b * L + p] when the loop returned (a bounded decode
+    # stopped by max_steps included; [MASK] where nothing was decoded)
+    x_final: np.ndarray = field(default=None, repr=False)
 
 
 class _Seq:
@@ -181,8 +184,8 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     max_steps: stop after this many denoising steps (benchmarking a bounded sample;
         stats.decoded then counts the tokens decoded so far).
     device_schedule: keep the decode's bookkeeping on the device (fdl.device_decode; one
-        host synchronisation per step). Needs the HIP driver on a GPU, the fixed-stride layout,
-        the device ranking and no tokenizer; the decisions are the same.
+        host synchronisation per step). Needs the HIP driver on a GPU, the device ranking and
+        no tokenizer; the decisions are the same, with or without kv_pages.
     kv_pages: K/V caches as a pool of this many 32-slot pages (None: the fixed stride of L
         slots per sequence). A sequence starts with the pages of its seqlen_k key slots and
         gets more when its masked block reaches past them; admission reserves pages up to
@@ -198,15 +201,15 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     cfg = model.config
     stats = stats if stats is not None else DecodeStats()
     if device_schedule:
-        if (torch.device(dev).type != "cuda" or kv_pages is not None or tokenizer is not None
+        if (torch.device(dev).type != "cuda" or tokenizer is not None
                 or not use_gpu_rank or not rows_only or not _accepts_logit_rows(model)):
-            raise ValueError("device_schedule needs a GPU model with logit rows, the fixed-stride "
-                             "cache layout, the device ranking and no tokenizer")
+            raise ValueError("device_schedule needs a GPU model with logit rows, the device "
+                             "ranking and no tokenizer")
         from .device_decode import generate_device_scheduled
         return generate_device_scheduled(model, prompts, prompt_lengths, batch_size, responses,
                                          n_steps, gen_length, block_length, mask_id, threshold,
                                          gamma, track_num, mask_num, eos_id, verify, stats,
-                                         max_steps)
+                                         max_steps, kv_pages)
     bm = block_length
     bn = 128
     B = batch_size
@@ -223,11 +226,9 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     PL = DEFAULT_PAGE_LOG2
     if paged:
         pool = PagePool(kv_pages, PL)
-        page_table = np.zeros((B, L >> PL), dtype=np.int32)
+        rows_p = PagedRows(pool, B, L)
+        page_table = rows_p.page_table
         n_slots = pool.n_slots
-        logical_of = np.full(n_slots, -1, dtype=np.int64)  # pool slot -> j * L + p
-        seq_pages = [np.zeros(0, np.int32) for _ in range(B)]
-        reserved = [0] * B  # pages promised to row j beyond the ones it holds
     else:
         page_table = contiguous_page_table(B, L)
         n_slots = B * L
@@ -244,28 +245,11 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
 
     def pages_needed(i: int) -> int:
         """Pages reserved at admission (positions a decode normally reaches)."""
-        span = max(seqlen_k_of(i), int(prompt_lengths[i]) + gen_length + bm - 1)
-        return pool.pages_for(min(L, span))
-
-    def grow(j: int, n_positions: int) -> None:
-        """Gives row j pages for logical positions 0 .. n_positions - 1."""
-        have = seq_pages[j].size
-        need = pool.pages_for(n_positions)
-        if need <= have:
-            return
-        extra = pool.alloc(need - have, above=int(seq_pages[j].max()) if have else -1)
-        reserved[j] = max(0, reserved[j] - extra.size)
-        page_table[j, have:need] = extra
-        seq_pages[j] = np.concatenate([seq_pages[j], extra])
-        logical_of[page_slots(extra, extra.size << PL, PL)] = \
-            j * L + (have << PL) + np.arange(extra.size << PL)
+        return pages_reserved(pool, L, seqlen_k_of(i), int(prompt_lengths[i]), gen_length, bm)
 
     def phys(a: np.ndarray) -> np.ndarray:
         """Cache slots of logical slots j * L + p."""
-        if not paged:
-            return a
-        j, p = np.divmod(a, L)
-        return (page_table[j, p >> PL].astype(np.int64) << PL) | (p & ((1 << PL) - 1))
+        return rows_p.phys(a) if paged else a
 
     def idle(j: int) -> None:
         s = seqs[j]
@@ -276,11 +260,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
 
     def release(j: int) -> None:
         if paged:
-            reserved[j] = 0
-            if seq_pages[j].size:
-                logical_of[page_slots(seq_pages[j], seq_pages[j].size << PL, PL)] = -1
-                pool.free(seq_pages[j])
-                seq_pages[j] = np.zeros(0, np.int32)
+            rows_p.release(j)
 
     def admit(j: int) -> bool:
         """Loads the next prompt into row j if there is one and its pages fit."""
@@ -289,11 +269,9 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
             return False
         if paged:
             need = pages_needed(count)
-            if pool.n_free - sum(reserved) < need:
+            if not rows_p.fits(need):
                 return False
-            page_table[j] = 0
-            reserved[j] = need
-            grow(j, seqlen_k_of(count))
+            rows_p.admit(j, need, seqlen_k_of(count))
         load_prompt(j, count)
         count += 1
         return True
@@ -396,7 +374,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     hi = max(int(s.masked.max()) if len(s.masked) else -1,
                              int(s.tracked.max()) if len(s.tracked) else -1)
                     if hi >= 0:
-                        grow(j, hi - j * L + 1)
+                        rows_p.grow(j, hi - j * L + 1)
         # ---- pack the step's query rows: masked rows, then tracked rows (:439-467)
         masked_blocks, tracked_blocks, seq_rows = [], [], []
         acc = 0
@@ -635,7 +613,7 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
                     if n != rank_len[j]:
                         raise RuntimeError(f"ranked {rank_len[j]} slots of sequence {j}, "
                                            f"the refresh reads {n}")
-                    full_pos[j, :n] = logical_of[fp[j, :n]] if paged else fp[j, :n]
+                    full_pos[j, :n] = rows_p.logical_of[fp[j, :n]] if paged else fp[j, :n]
             else:
                 sc = attn_scores.cpu().numpy()
                 for j in cont:
@@ -667,4 +645,5 @@ def generate_with_Flash_dLLM(model, prompts, prompt_lengths, batch_size, respons
     if torch.device(dev).type == "cuda":
         torch.cuda.synchronize(dev)
     stats.wall_s = time.perf_counter() - t_start
+    stats.x_final = x.copy()
     return responses, num_tokens, max_num_tokens

@@ -138,7 +138,7 @@ SIGNATURES: dict[str, tuple] = {
 # fdl_sched (include/fdl.h): device pointers, sizes and parameters of the device scheduler
 SCHED_SEQ_FIELDS = 16
 SEQ_ACTIVE, SEQ_ND, SEQ_SEQLEN_K, SEQ_PRED, SEQ_EOS, SEQ_N_MASKED, SEQ_KEEP, SEQ_T, SEQ_S, \
-    SEQ_DONE, SEQ_N_TRACKED, SEQ_T0, SEQ_T1, SEQ_FRESH, SEQ_ERR = range(15)
+    SEQ_DONE, SEQ_N_TRACKED, SEQ_T0, SEQ_T1, SEQ_FRESH, SEQ_ERR, SEQ_HI = range(16)
 SCHED_SUMMARY_FIELDS = 16
 SUM_Q, SUM_N_MASKED_ROWS, SUM_N_LONG, SUM_N_MID, SUM_N_SHORT, SUM_N_CONT, SUM_N_DONE, \
     SUM_OVERFLOW, SUM_DECODED, SUM_VERIFY_ACCEPTED = range(10)

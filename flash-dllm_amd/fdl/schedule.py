@@ -102,6 +102,73 @@ class PagePool:
         self._free[pages] = True
 
 
+class PagedRows:
+    """The rows of a decode batch over a PagePool: row j's page-table row (pages for its
+    logical positions 0 .. 2^page_log2 * n_j - 1), the pages promised to it at admission
+    beyond the ones it holds, and the pool slot -> logical slot (j * L + p) table. Shared by
+    the host-scheduled and the device-scheduled decode loops (fdl.generate,
+    fdl.device_decode), so both admit and grow rows identically."""
+
+    def __init__(self, pool: PagePool, n_rows: int, max_length: int):
+        self.pool = pool
+        self.L = max_length
+        self.PL = pool.page_log2
+        self.page_table = np.zeros((n_rows, max_length >> self.PL), dtype=np.int32)
+        self.logical_of = np.full(pool.n_slots, -1, dtype=np.int64)
+        self.pages = [np.zeros(0, np.int32) for _ in range(n_rows)]
+        self.reserved = [0] * n_rows
+        self.version = 0  # changes with every page handed out or returned
+
+    def fits(self, n_pages: int) -> bool:
+        """A reservation of n_pages fits beside the ones promised to the other rows."""
+        return self.pool.n_free - sum(self.reserved) >= n_pages
+
+    def admit(self, j: int, reserve: int, n_positions: int) -> None:
+        """Row j starts a sequence: `reserve` pages promised, n_positions covered now."""
+        self.page_table[j] = 0
+        self.reserved[j] = reserve
+        self.grow(j, n_positions)
+
+    def grow(self, j: int, n_positions: int) -> None:
+        """Gives row j pages for logical positions 0 .. n_positions - 1: from its reservation
+        first, ids above its last page first (slot order then follows position order)."""
+        have = self.pages[j].size
+        need = self.pool.pages_for(n_positions)
+        if need <= have:
+            return
+        extra = self.pool.alloc(need - have, above=int(self.pages[j].max()) if have else -1)
+        self.reserved[j] = max(0, self.reserved[j] - extra.size)
+        self.page_table[j, have:need] = extra
+        self.pages[j] = np.concatenate([self.pages[j], extra])
+        self.logical_of[page_slots(extra, extra.size << self.PL, self.PL)] = \
+            j * self.L + (have << self.PL) + np.arange(extra.size << self.PL)
+        self.version += 1
+
+    def release(self, j: int) -> None:
+        """Row j's sequence finished: its pages return to the pool."""
+        self.reserved[j] = 0
+        if self.pages[j].size:
+            self.logical_of[page_slots(self.pages[j], self.pages[j].size << self.PL, self.PL)] = -1
+            self.pool.free(self.pages[j])
+            self.pages[j] = np.zeros(0, np.int32)
+            self.version += 1
+
+    def phys(self, a: np.ndarray) -> np.ndarray:
+        """Pool slots of logical slots j * L + p."""
+        j, p = np.divmod(a, self.L)
+        return (self.page_table[j, p >> self.PL].astype(np.int64) << self.PL) | \
+            (p & ((1 << self.PL) - 1))
+
+
+def pages_reserved(pool: PagePool, max_length: int, seqlen_k: int, prompt_len: int,
+                   gen_length: int, block_m: int) -> int:
+    """Pages a sequence is promised at admission: its seqlen_k keys, or up to
+    prompt + gen + block_m - 1 positions (how far a masked block reaches while no token past
+    prompt + gen is accepted ahead of earlier ones), within the row of max_length slots."""
+    span = max(seqlen_k, prompt_len + gen_length + block_m - 1)
+    return pool.pages_for(min(max_length, span))
+
+
 def build_work(seqs: list[SeqRows], max_rows: int = MAX_TILE_ROWS, mid_rows: int = MID_TILE_ROWS,
                long_rows: int = LONG_TILE_ROWS) -> tuple[np.ndarray, np.ndarray, int, int]:
     """Splits each sequence's rows into tiles of three classes.

@@ -336,6 +336,8 @@ enum fdl_sched_seq_field {
   FDL_SEQ_T1 = 12,
   FDL_SEQ_FRESH = 13,     /* 1: the next step recomputes every slot (step 0 of a prompt) */
   FDL_SEQ_ERR = 14,       /* 1: fewer decoded slots than verify fill rows */
+  FDL_SEQ_HI = 15,        /* highest position (p of slot j * L + p) the next step's rows
+                             query, -1: none (a paged pool grows the row's pages to it) */
   FDL_SCHED_SEQ_FIELDS = 16,
 };
 /* summary int32 [FDL_SCHED_SUMMARY_FIELDS], written by fdl_sched_pack (DECODED and

@@ -261,3 +261,14 @@ def test_validate_vblocks():
     _expect(lib.FDL_ERR_RANGE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 7)   # 8 rows > 7
     lib.call("fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 256)   # 2 * block_m up to 256
     _expect(lib.FDL_ERR_SHAPE, "fdl_validate_vblocks", vp, 2, kp, 5, 16, 11, 257)
+
+
+def test_scheduler_record_fields_match_the_header():
+    """The per-sequence and summary field indices the binding uses are the header's enums."""
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "fdl.h").read_text()
+    fields = {m.group(1): int(m.group(2))
+              for m in re.finditer(r"FDL_(SEQ_[A-Z0-9_]+|SUM_[A-Z0-9_]+) = (\d+)", hdr)}
+    assert fields.pop("SEQ_HI") == lib.SEQ_HI == 15
+    for name, value in fields.items():
+        assert getattr(lib, name) == value, name
+    assert re.search(r"FDL_SCHED_SEQ_FIELDS = (\d+)", hdr).group(1) == str(lib.SCHED_SEQ_FIELDS)

@@ -359,6 +359,43 @@ def test_paged_pool_decode_matches_fixed_stride_on_gpu(verify):
     assert out[0] == out[1]
 
 
+@pytest.mark.parametrize("eos", [2045, 2047])
+@pytest.mark.parametrize("verify", [False, True])
+def test_device_schedule_paged_pool(verify, eos):
+    """The device-scheduled decode over a paged K/V pool (fdl_sched_* bookkeeping in logical
+    slots; pages grown at each step's synchronisation to the highest position the next rows
+    query, FDL_SEQ_HI; K/V write slots, verify keys and the ranking mapped through the page
+    table on the device): with pages for every row it is the fixed-stride decode token for
+    token, with the same step counts; with a pool too small for all rows at once (prompts wait
+    for pages, refills reuse them) it is the host-scheduled decode over the same pool. Stride
+    L = ((96 + 48 + 16) // 128 + 1) * 128 = 256 slots = 8 pages per row; reservations of
+    4-8 pages. EOS 2047 is never emitted: sequences decode past prompt + gen into the EOS
+    padding and grow beyond their reservations, page by page."""
+    model = _model(lm_head_std=1.0, seed=6)
+    rng = np.random.default_rng(8)
+    lengths = [64, 96, 79, 80, 64]
+    prompts = [torch.from_numpy(rng.integers(0, 2000, n)) for n in lengths]
+    kw = dict(gen_length=48, block_length=16, mask_id=2046, threshold=0.9, gamma=0.9,
+              track_num=1, mask_num=1, eos_id=eos, verify=verify)
+    runs = {}
+    for name, pages, dev_sched in (("fixed", None, False), ("fixed_device", None, True),
+                                   ("full_device", 24, True), ("tight_host", 12, False),
+                                   ("tight_device", 12, True)):
+        st, steps = DecodeStats(), [0] * 5
+        r, n, m = generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, steps,
+                                           stats=st, kv_pages=pages, device_schedule=dev_sched,
+                                           **kw)
+        runs[name] = (r, n, m, steps)
+        print(f"{name}: steps {steps}, host syncs {st.host_syncs}, decoded {st.decoded}",
+              flush=True)
+    assert runs["fixed_device"] == runs["fixed"]
+    assert runs["full_device"] == runs["fixed"]
+    assert runs["tight_device"] == runs["tight_host"]
+    with pytest.raises(MemoryError):
+        generate_with_Flash_dLLM(model, prompts, lengths, 3, [None] * 5, [0] * 5, kv_pages=7,
+                                 device_schedule=True, **kw)
+
+
 @pytest.mark.parametrize("verify,block,lengths", [
     (False, 32, [96, 128, 100, 72, 80]),
     (True, 32, [96, 128, 100, 72, 80]),
