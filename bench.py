@@ -269,12 +269,22 @@ def _capture(fn, reps: int):
     return g
 
 
-def _graph_time(fn, reps: int, replays: int = 3) -> float:
-    """Mean microseconds per call of fn() replayed from a graph of `reps` calls."""
+CLOCK_WARM_S = 0.2
+
+
+def _graph_time(fn, reps: int, replays: int = 3, warm_s: float = CLOCK_WARM_S) -> float:
+    """Mean microseconds per call of fn() replayed from a graph of `reps` calls. Before the
+    timed replays the graph is replayed, untimed, for warm_s seconds: the shader clock ramps
+    up over the first ~0.1 s of sustained load (a 8 x 1024-row full-recompute attention reads
+    190 us on its first replays and 160 us from then on)."""
     import torch
     g = _capture(fn, reps)
-    g.replay()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while True:
+        g.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(replays):
@@ -1028,6 +1038,11 @@ def main() -> int:
     us_eager = r["total_ms"] * 1e3 / args.steps
     qkv_f, qkv_b = cnt["qkv"]
     attn_f, attn_b = cnt["attn"]
+    # in-step durations: the whole step's graph time split in proportion to the kernels'
+    # alone times (kernels.*.us sum to graph_step_us; the alone times are in kernel_timing)
+    alone = dict(per)
+    share = r["graph_step_us"] / sum(alone.values())
+    per = {n: alone[n] * share for n in alone}
     t_qkv, t_attn = per["qkv_rope_cache"], per["block_attention"]
     kernels = {
         "qkv_rope_cache": {"us": t_qkv, "TFLOP/s": qkv_f / t_qkv / 1e6, "GB/s": qkv_b / t_qkv / 1e3,
@@ -1044,6 +1059,10 @@ def main() -> int:
     cold = r["cold"]
     cold_line = None
     if cold:
+        # the cold step's graph time split in proportion to the kernels' cold alone times
+        c_alone = {n: cold[n] for n in kernels}
+        c_share = cold["graph_step_us"] / sum(c_alone.values())
+        cold = dict(cold, **{n: c_alone[n] * c_share for n in kernels})
         c_qkv, c_attn = cold["qkv_rope_cache"], cold["block_attention"]
         c_ach = qkv_f / c_qkv / 1e6
         cold_line = {
@@ -1059,8 +1078,8 @@ def main() -> int:
                                    "mfma_frac": round(qkv_f / c_qkv / 1e6 / PEAK_BF16_TFLOPS, 4)},
                 "block_attention": {"us": round(c_attn, 3),
                                     "hbm_frac": round(attn_b / c_attn / 1e3 / PEAK_HBM_GBS, 4)},
-                "importance_accumulate_rank": {"us": round(cold["importance_accumulate_rank"], 3)},
-                "sum_us": round(sum(cold[n] for n in kernels), 3)},
+                "importance_accumulate_rank": {"us": round(cold["importance_accumulate_rank"], 3)}},
+            "alone_us": {k: round(v, 3) for k, v in c_alone.items()},
         }
     out = {
         "metric": METRIC,
@@ -1091,11 +1110,16 @@ def main() -> int:
         "roofline_cold_cache": None if cold_line is None else cold_line["roofline"],
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
         "eager_us_per_step": round(us_eager, 2),
-        "kernel_timing": {"how": "each kernel alone: --steps back-to-back calls in one HIP graph, "
-                                 "replayed 3 times, HIP events around the replays on the kernels' "
-                                 "stream (in-sequence duration including one kernel boundary); "
-                                 "additive: kernels_sum_us against graph_step_us of the whole step",
-                          "kernels_sum_us": round(sum(per[n] for n in kernels), 3),
+        "kernel_timing": {"how": "alone_us: each kernel alone, --steps back-to-back calls in one "
+                                 "HIP graph, replayed 3 times, HIP events around the replays on the "
+                                 "kernels' stream (in-sequence duration including one kernel "
+                                 "boundary); kernels.*.us: graph_step_us (the whole step's graph) "
+                                 "split in proportion to alone_us, so they add up to the step; "
+                                 "every graph is replayed untimed for clock_warm_s before its "
+                                 "timed replays (the shader clock ramps up under sustained load)",
+                          "clock_warm_s": CLOCK_WARM_S,
+                          "alone_us": {k: round(v, 3) for k, v in alone.items()},
+                          "alone_sum_us": round(sum(alone.values()), 3),
                           "graph_step_us": round(r["graph_step_us"], 3),
                           "graph_matches_eager": r["graph_matches_eager"],
                           "events_around_eager_launches_us": {

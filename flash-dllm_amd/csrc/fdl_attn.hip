@@ -1029,6 +1029,46 @@ struct LongState {
   f32x4 o[2][8];
 };
 
+// Phase fences of the ping-pong. The barrier between a wavefront's MFMA phase and its
+// softmax phase is an asm with a memory clobber, which orders memory operations only: the
+// scheduler may move register-only work across it (it sank the exponentials, the bf16
+// conversions and the row sums of a softmax phase into the next MFMA phase, next to the
+// other group's softmax). An empty asm that reads a value ("v") makes the value final
+// before it; one that "writes" a value ("+v") keeps every later use of the value after it.
+// Both emit no instruction.
+__device__ __forceinline__ void settle(const f32x4 (&v)[2][4]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" ::"v"(v[i][j]));
+}
+__device__ __forceinline__ void hold(f32x4 (&v)[2][4]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(v[i][j]));
+}
+__device__ __forceinline__ void settle(const bf16x8 (&v)[2][2]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) asm volatile("" ::"v"(v[i][j]));
+}
+__device__ __forceinline__ void hold(bf16x8 (&v)[2][2]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(v[i][j]));
+}
+__device__ __forceinline__ void settle(const LongState& st) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    asm volatile("" ::"v"(st.m[i]), "v"(st.l[i]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(st.o[i][j]));
+  }
+}
+
 // V^T fragment i = 8 ks + db of the fragment-major buffer: one 16-byte read per lane.
 __device__ __forceinline__ bf16x8 vtf_frag(const u32x4* vtf, int i, int lane) {
   return as_bf16x8(vtf[i * 64 + lane]);
@@ -1358,8 +1398,9 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
     return reinterpret_cast<const u32x4*>(smem + (p % kLongStages) * kStageBytes);
   };
   auto vt_of = [&](int p) -> const u32x4* { return vtb[p & 1]; };
-  auto transpose = [&](int p) {
-    transpose_v(smem + (p % kLongStages) * kStageBytes + kTileBytes, vtb[p & 1], wave, lane);
+  // V block p into the fragment-major V^T buffer of its parity, fragments 4 wq .. 4 wq + 3
+  auto transpose = [&](int p, int wq) {
+    transpose_v(smem + (p % kLongStages) * kStageBytes + kTileBytes, vtb[p & 1], wq, lane);
   };
 
   {
@@ -1411,21 +1452,26 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
           long_softmax<true>(st, sc, pb, sl2, k_end - k_begin, g);
         else
           long_softmax<false>(st, sc, pb, sl2, kTileN, g);
-        transpose(0);
+        transpose(0, wave);
         if (n_blk > 1) wait_next(0);
         barrier_only();
         for (int p = 1; p < n_blk - 1; ++p) {
+          hold(pb);
           long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
           imp_block(p);
+          settle(sc);
+          settle(st);
           barrier_only();
+          hold(sc);
           // into the stage of block p - 1, released in pair p - 1: one share before the
           // softmax, the other after the transpose (each issue may wait for room in the
           // load queue)
           if (p + 2 < n_blk) issue(p + 2, wave);
           long_softmax<false>(st, sc, pb, sl2, kTileN, g);
-          transpose(p);
           if (p + 2 < n_blk) issue(p + 2, wave + 4);
           wait_next(p);
+          settle(pb);
+          settle(st);
           barrier_only();
         }
         if (n_blk > 1) {
@@ -1434,7 +1480,6 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
           imp_block(p);
           barrier_only();
           long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * p), g);
-          transpose(p);
           barrier_only();
         }
         long_pv(st, pb, vt_of(n_blk - 1), lane);
@@ -1451,10 +1496,19 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
       if (n_blk > 1) wait_next(0);
       barrier_only();
       for (int p = 1; p < n_blk; ++p) {
+        hold(sc);
         long_softmax<false>(st, sc, pb, sl2, kTileN, g);
+        settle(pb);
+        settle(st);
         barrier_only();
+        hold(pb);
         long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
+        // V block p to V^T next to this MFMA phase (the other group's softmax phase then
+        // holds only the softmax and the block loads)
+        transpose(p, wave - 4);
         if (p + 1 < n_blk) wait_next(p);
+        settle(sc);
+        settle(st);
         barrier_only();
       }
       long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * (n_blk - 1)), g);
