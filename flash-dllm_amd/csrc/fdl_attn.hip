@@ -1033,15 +1033,10 @@ struct LongState {
 // softmax phase is an asm with a memory clobber, which orders memory operations only: the
 // scheduler may move register-only work across it (it sank the exponentials, the bf16
 // conversions and the row sums of a softmax phase into the next MFMA phase, next to the
-// other group's softmax). An empty asm that reads a value ("v") makes the value final
-// before it; one that "writes" a value ("+v") keeps every later use of the value after it.
-// Both emit no instruction.
-__device__ __forceinline__ void settle(const f32x4 (&v)[2][4]) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) asm volatile("" ::"v"(v[i][j]));
-}
+// other group's softmax). settle(P) (an empty asm reading the probabilities) makes the
+// softmax final before the barrier that ends its phase; hold(S) (one that "writes" the
+// logits) keeps the softmax after the barrier that starts it. Both emit no instruction.
+// (Fencing the MFMA results as well was measured 1-3% slower.)
 __device__ __forceinline__ void hold(f32x4 (&v)[2][4]) {
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -1053,20 +1048,6 @@ __device__ __forceinline__ void settle(const bf16x8 (&v)[2][2]) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) asm volatile("" ::"v"(v[i][j]));
-}
-__device__ __forceinline__ void hold(bf16x8 (&v)[2][2]) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(v[i][j]));
-}
-__device__ __forceinline__ void settle(const LongState& st) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    asm volatile("" ::"v"(st.m[i]), "v"(st.l[i]));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(st.o[i][j]));
-  }
 }
 
 // V^T fragment i = 8 ks + db of the fragment-major buffer: one 16-byte read per lane.
@@ -1456,11 +1437,8 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
         if (n_blk > 1) wait_next(0);
         barrier_only();
         for (int p = 1; p < n_blk - 1; ++p) {
-          hold(pb);
           long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
           imp_block(p);
-          settle(sc);
-          settle(st);
           barrier_only();
           hold(sc);
           // into the stage of block p - 1, released in pair p - 1: one share before the
@@ -1471,7 +1449,6 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
           if (p + 2 < n_blk) issue(p + 2, wave + 4);
           wait_next(p);
           settle(pb);
-          settle(st);
           barrier_only();
         }
         if (n_blk > 1) {
@@ -1499,16 +1476,12 @@ __global__ __launch_bounds__(512, 1) void attn_long_kernel(AttnArgs a) {
         hold(sc);
         long_softmax<false>(st, sc, pb, sl2, kTileN, g);
         settle(pb);
-        settle(st);
         barrier_only();
-        hold(pb);
         long_pv_qk(st, pb, vt_of(p - 1), sc, qf, kt_of(p), lane);
         // V block p to V^T next to this MFMA phase (the other group's softmax phase then
         // holds only the softmax and the block loads)
         transpose(p, wave - 4);
         if (p + 1 < n_blk) wait_next(p);
-        settle(sc);
-        settle(st);
         barrier_only();
       }
       long_softmax<true>(st, sc, pb, sl2, k_end - (k_begin + kTileN * (n_blk - 1)), g);
