@@ -1038,11 +1038,9 @@ def main() -> int:
     us_eager = r["total_ms"] * 1e3 / args.steps
     qkv_f, qkv_b = cnt["qkv"]
     attn_f, attn_b = cnt["attn"]
-    # in-step durations: the whole step's graph time split in proportion to the kernels'
-    # alone times (kernels.*.us sum to graph_step_us; the alone times are in kernel_timing)
+    # per-kernel durations: each kernel alone in its own graph (additive: their sum is at most
+    # the whole step's graph time, the rest being the kernel boundaries of the step)
     alone = dict(per)
-    share = r["graph_step_us"] / sum(alone.values())
-    per = {n: alone[n] * share for n in alone}
     t_qkv, t_attn = per["qkv_rope_cache"], per["block_attention"]
     kernels = {
         "qkv_rope_cache": {"us": t_qkv, "TFLOP/s": qkv_f / t_qkv / 1e6, "GB/s": qkv_b / t_qkv / 1e3,
@@ -1059,10 +1057,6 @@ def main() -> int:
     cold = r["cold"]
     cold_line = None
     if cold:
-        # the cold step's graph time split in proportion to the kernels' cold alone times
-        c_alone = {n: cold[n] for n in kernels}
-        c_share = cold["graph_step_us"] / sum(c_alone.values())
-        cold = dict(cold, **{n: c_alone[n] * c_share for n in kernels})
         c_qkv, c_attn = cold["qkv_rope_cache"], cold["block_attention"]
         c_ach = qkv_f / c_qkv / 1e6
         cold_line = {
@@ -1079,7 +1073,7 @@ def main() -> int:
                 "block_attention": {"us": round(c_attn, 3),
                                     "hbm_frac": round(attn_b / c_attn / 1e3 / PEAK_HBM_GBS, 4)},
                 "importance_accumulate_rank": {"us": round(cold["importance_accumulate_rank"], 3)}},
-            "alone_us": {k: round(v, 3) for k, v in c_alone.items()},
+            "kernels_sum_us": round(sum(cold[n] for n in kernels), 3),
         }
     out = {
         "metric": METRIC,
@@ -1110,16 +1104,15 @@ def main() -> int:
         "roofline_cold_cache": None if cold_line is None else cold_line["roofline"],
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
         "eager_us_per_step": round(us_eager, 2),
-        "kernel_timing": {"how": "alone_us: each kernel alone, --steps back-to-back calls in one "
-                                 "HIP graph, replayed 3 times, HIP events around the replays on the "
-                                 "kernels' stream (in-sequence duration including one kernel "
-                                 "boundary); kernels.*.us: graph_step_us (the whole step's graph) "
-                                 "split in proportion to alone_us, so they add up to the step; "
-                                 "every graph is replayed untimed for clock_warm_s before its "
-                                 "timed replays (the shader clock ramps up under sustained load)",
+        "kernel_timing": {"how": "kernels.*.us: each kernel alone, --steps back-to-back calls in "
+                                 "one HIP graph, replayed 3 times, HIP events around the replays on "
+                                 "the kernels' stream (in-sequence duration, kernel boundaries "
+                                 "included); additive: kernels_sum_us against graph_step_us, the "
+                                 "whole step's graph time per step; every graph is replayed untimed "
+                                 "for clock_warm_s before its timed replays (the shader clock ramps "
+                                 "up under sustained load)",
                           "clock_warm_s": CLOCK_WARM_S,
-                          "alone_us": {k: round(v, 3) for k, v in alone.items()},
-                          "alone_sum_us": round(sum(alone.values()), 3),
+                          "kernels_sum_us": round(sum(alone.values()), 3),
                           "graph_step_us": round(r["graph_step_us"], 3),
                           "graph_matches_eager": r["graph_matches_eager"],
                           "events_around_eager_launches_us": {
