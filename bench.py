@@ -207,6 +207,11 @@ def run_gpu(steps: int, warmup: int, seed: int = 2, cold_cache: bool = True):
     # per-kernel durations, additive: each kernel alone, `steps` back-to-back calls in one
     # HIP graph, replayed (its in-sequence duration including one kernel boundary)
     per = {n: _graph_time(steps_of([n]), steps) for n in names}
+    # the projection as one plain library GEMM of the same shape (hipBLASLt through torch; no
+    # RoPE, no cache scatter): the bar the fused kernel is compared with
+    w_cat = torch.cat([d["wq"], d["wk"], d["wv"]], dim=0)
+    blas_us = _graph_time(lambda: torch.nn.functional.linear(d["x"], w_cat), steps)
+    del w_cat
     # cold Infinity Cache: the same graphs with the weights and the K/V cache rotating over
     # four copies (4 x 213 MB, past the 256 MB Infinity Cache), so that every launch reads
     # them from HBM, as in a multi-layer forward (each layer's weights and cache read once)
@@ -249,6 +254,7 @@ def run_gpu(steps: int, warmup: int, seed: int = 2, cold_cache: bool = True):
         if not same:
             break
     return dict(Q=Q, total_ms=total_ms, per_kernel_us=per, per_kernel_events_us=per_events,
+                blas_us=blas_us,
                 graph_matches_eager=same, graph_step_us=graph_step, graph_total_ms=graph_k_steps_ms,
                 cold=cold)
 
@@ -540,6 +546,10 @@ def run_configs(reps: int = 10) -> dict:
     plan.validate(Q, st["n_slots"])
     t_qkv, e_qkv = _op_times(lambda: ops.qkv_rope_cache(x, *w, sin, cos, slots, q, kc, vc, H,
                                                         rope_row=rope_row), reps)
+    # the same product as one plain library GEMM (hipBLASLt through torch; no RoPE, no scatter)
+    w_cat = torch.cat(w, dim=0)
+    t_blas = _graph_time(lambda: torch.nn.functional.linear(x, w_cat), reps)
+    del w_cat
     t_att, e_att = _op_times(lambda: ops.block_attention(q, kc, vc, plan, att, H, scale,
                                                          lib.IMP_RAW_LOGIT, imp), reps)
     qk = np.array([len(sq.rows) for sq in st["seqs"]], dtype=np.float64)
@@ -552,10 +562,21 @@ def run_configs(reps: int = 10) -> dict:
                     f"{int(st['full'].sum())} full recomputes, {Q} query rows, raw-logit importance",
         "qkv_rope_cache": {"us": round(t_qkv, 2), "TFLOP/s": round(f_qkv / t_qkv / 1e6, 1),
                            "mfma_frac": round(f_qkv / t_qkv / 1e6 / PEAK_BF16_TFLOPS, 4),
-                           "eager_us": round(e_qkv, 2)},
+                           "eager_us": round(e_qkv, 2),
+                           "hipblaslt_gemm_us": round(t_blas, 2),
+                           "hipblaslt_mfma_frac": round(f_qkv / t_blas / 1e6 / PEAK_BF16_TFLOPS, 4)},
         "block_attention": {"us": round(t_att, 2), "TFLOP/s": round(f_att / t_att / 1e6, 1),
                             "GB/s": round(b_att / t_att / 1e3, 1), "eager_us": round(e_att, 2)},
     }
+    # the partial sequences alone (64- and 128-row tiles, HBM-bound)
+    pseqs = [sq for sq in st["seqs"] if len(sq.rows) != sq.k_end]
+    pplan = make_plan(pseqs, st["table"], 5, device=dev)
+    t_part = _graph_time(lambda: ops.block_attention(q, kc, vc, pplan, att, H, scale,
+                                                     lib.IMP_RAW_LOGIT, imp), reps)
+    b_part = float(sum(2.0 * len(sq.rows) * D * 2 + 2.0 * sq.k_end * D * 2 for sq in pseqs))
+    out["block_table_stress"]["partial_attention"] = {
+        "sequences": len(pseqs), "us": round(t_part, 2), "GB/s": round(b_part / t_part / 1e3, 1),
+        "hbm_frac": round(b_part / t_part / 1e3 / PEAK_HBM_GBS, 4)}
     fseqs = [sq for sq in st["seqs"] if len(sq.rows) == sq.k_end]
     if fseqs:
         fplan = make_plan(fseqs, st["table"], 5, device=dev)
@@ -990,6 +1011,68 @@ def run_cpu_e2e_step(model_gpu, tokens_per_step: float, seed: int = 0) -> dict:
                       "decode's steady state"}
 
 
+def run_one_kernel(name: str, launches: int) -> int:
+    """One kernel's workload alone, for counter profiles: 0.5 s of untimed launches (warm
+    clock), then `launches` timed ones (HIP events around them; one JSON line).
+      full_recompute_8x1024  block attention of 8 sequences x 1024 rows over their 1024 keys
+                             (256-row tiles, no importance), 32 heads
+      block_attention        the single-layer workload's block attention (64-row tiles,
+                             softmax-colsum importance)
+      qkv_rope_cache         the single-layer workload's fused projection (512 rows)"""
+    import torch
+    from fdl import lib, ops
+    from fdl.schedule import SeqRows, contiguous_page_table, make_plan
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(0)
+    scale = 1.0 / np.sqrt(HD)
+    if name == "full_recompute_8x1024":
+        Lk = 1024
+        kc = torch.randn((8 * Lk, D), generator=gen).to(torch.bfloat16).to(dev)
+        vc = torch.randn((8 * Lk, D), generator=gen).to(torch.bfloat16).to(dev)
+        q = torch.randn((8 * Lk, D), generator=gen).to(torch.bfloat16).to(dev)
+        out = torch.empty_like(q)
+        plan = make_plan([SeqRows(b, Lk, np.arange(b * Lk, (b + 1) * Lk)) for b in range(8)],
+                         contiguous_page_table(8, Lk), device=dev)
+        fn = lambda: ops.block_attention(q, kc, vc, plan, out, H, scale)  # noqa: E731
+        work, unit = 8 * 4.0 * Lk * Lk * D, "flop"
+    else:
+        host, d = build_workload(2, dev)
+        Q = len(host["slots"])
+        kc = torch.randn((B * L, D), generator=gen).to(torch.bfloat16).to(dev)
+        vc = torch.randn_like(kc)
+        q = torch.empty((Q, D), dtype=torch.bfloat16, device=dev)
+        att = torch.empty_like(q)
+        imp = torch.zeros((H, B * L), dtype=torch.float32, device=dev)
+        cnt = algorithmic_counts(Q)
+        if name == "block_attention":
+            q.copy_(d["x"])
+            fn = lambda: ops.block_attention(q, kc, vc, d["plan"], att, H, scale,  # noqa: E731
+                                             lib.IMP_SOFTMAX_COLSUM, imp)
+            work, unit = cnt["attn"][1], "byte"
+        elif name == "qkv_rope_cache":
+            fn = lambda: ops.qkv_rope_cache(d["x"], d["wq"], d["wk"], d["wv"], d["sin"],  # noqa: E731
+                                            d["cos"], d["slot"], q, kc, vc, H)
+            work, unit = cnt["qkv"][0], "flop"
+        else:
+            print(f"unknown kernel workload {name}", file=sys.stderr)
+            return 2
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.5:
+        fn()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(launches):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    frac = work / us / 1e6 / PEAK_BF16_TFLOPS if unit == "flop" else work / us / 1e3 / PEAK_HBM_GBS
+    print(json.dumps({"kernel_workload": name, "us": round(us, 2), "launches": launches,
+                      ("mfma_frac" if unit == "flop" else "hbm_frac"): round(frac, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description="Flash-Cache hot-path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -1014,11 +1097,17 @@ def main() -> int:
                     help="bound the HIP decode to this many steps (default: run to completion)")
     ap.add_argument("--e2e-torch-steps", type=int, default=24,
                     help="steps of the unfused PyTorch driver decode (0: skip)")
+    ap.add_argument("--kernel", default=None,
+                    help="run only one kernel's workload (full_recompute_8x1024, block_attention, "
+                         "qkv_rope_cache) for --steps launches after a warm-up, for counter "
+                         "profiles")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.kernel:
+        return run_one_kernel(args.kernel, args.steps)
     r = run_gpu(args.steps, args.warmup, cold_cache=not args.no_cold)
     if args.copy_calibration:
         import torch
@@ -1044,7 +1133,9 @@ def main() -> int:
     t_qkv, t_attn = per["qkv_rope_cache"], per["block_attention"]
     kernels = {
         "qkv_rope_cache": {"us": t_qkv, "TFLOP/s": qkv_f / t_qkv / 1e6, "GB/s": qkv_b / t_qkv / 1e3,
-                           "mfma_frac": qkv_f / t_qkv / 1e6 / PEAK_BF16_TFLOPS},
+                           "mfma_frac": qkv_f / t_qkv / 1e6 / PEAK_BF16_TFLOPS,
+                           "hipblaslt_gemm_us": r["blas_us"],
+                           "hipblaslt_mfma_frac": qkv_f / r["blas_us"] / 1e6 / PEAK_BF16_TFLOPS},
         "block_attention": {"us": t_attn, "TFLOP/s": attn_f / t_attn / 1e6,
                             "GB/s": attn_b / t_attn / 1e3,
                             "hbm_frac": attn_b / t_attn / 1e3 / PEAK_HBM_GBS},
