@@ -982,15 +982,16 @@ __global__ __launch_bounds__(64 * (NC + kProducers), 1) void attn_kernel(AttnArg
 // each per SIMD. Every 64-key block j goes through an MFMA phase M_j (PV of block j-1, QK of
 // block j) and a softmax phase V_j; group B runs one half-step behind group A, so in every
 // half-step each SIMD has one wavefront issuing MFMAs and one running the softmax:
-//   half-step 2j:     A: M_j                        B: V_{j-1}
-//   half-step 2j + 1: A: V_j + transpose of V_j    B: M_j
+//   half-step 2j:     A: M_j                                B: V_{j-1}
+//   half-step 2j + 1: A: V_j + the loads of block j + 2     B: M_j + transpose of V_j
 // with a workgroup barrier between half-steps. Blocks move into a three-deep LDS ring (K and
-// row-major V of a block, 32 KB): in pair j each wavefront issues its quarter-block share of
-// the global -> LDS loads of block j + 2 at the start of its softmax phase, where it has
-// slack (an MFMA phase would stall on the issue). Group A rewrites each V block, after its
-// softmax, into a fragment-major V^T buffer (two, by block parity) from which both groups
-// read the O^T = V^T P^T operands with one 16-byte read per lane instead of two transposing
-// reads.
+// row-major V of a block, 32 KB). Every wavefront loads its share of the first three
+// blocks; later blocks are loaded by group A alone, in its softmax phase (an MFMA phase
+// would stall on the issue, and group B's softmax phase sits next to A's shorter MFMA
+// phase). Each V block is rewritten once (block 0 by group A, later blocks by group B after
+// its MFMA phase) into a fragment-major V^T buffer (two, by block parity) from which both
+// groups read the O^T = V^T P^T operands with one 16-byte read per lane instead of two
+// transposing reads.
 //
 // The loads are issued from inline assembly: the compiler then does not know them and
 // inserts no wait for them before unrelated LDS reads; the waves wait for their own loads
