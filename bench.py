@@ -23,7 +23,10 @@ graph, replayed (additive; their sum is reported beside the whole step's graph t
 value_cold_cache: the same layer with the weights and the K/V cache rotating over four
 copies, so that every launch reads HBM as in a 32-layer forward. The CPU baseline times the
 numpy oracle (the reference algorithm restated on the CPU) on a bounded sample of the same
-workload.
+workload. e2e_llada8b: the decode of a random-init LLaDA-8B (tokens/s), its greedy agreement
+with a float32 twin, and (greedy_agreement_trained) the same comparison on every position
+for a small model trained on a copy task in seconds on the GPU, whose logits are not near
+ties as random weights' are.
 """
 from __future__ import annotations
 
@@ -828,6 +831,7 @@ def run_e2e(max_steps: int | None, torch_steps: int, seed: int = 0, cpu_step: bo
                                       "PyTorch driver (every op a PyTorch op)"}
     if agreement_steps:
         out["greedy_agreement"] = run_e2e_agreement(model, prompts, lengths, kw, *agreement_steps)
+        out["greedy_agreement_trained"] = run_trained_agreement()
     if cpu_step:
         tps = _window(sth, 1, sth.steps)
         per_step = tps["tokens"] / max(tps["steps"], 1)
@@ -924,7 +928,58 @@ def run_e2e_agreement(model, prompts, lengths, kw, tf_steps: int, free_steps: in
             "steps": free_steps, "positions_decoded_by_both": int(both.sum()),
             "agreement": round(float(same.mean()), 4) if same.size else None},
         "north_star_bar": ">= 99% of positions; met on decisive rows, not on all rows (near-tied "
-                          "logits of random weights flip under any bf16 arithmetic)"}
+                          "logits of random weights flip under any bf16 arithmetic); on all "
+                          "positions for a trained model (greedy_agreement_trained)"}
+
+
+def run_trained_agreement() -> dict:
+    """Greedy agreement on every position for a trained model: fdl.copy_task trains a small
+    LLaDA-shaped model (2 layers, d_model 256, two heads of 128, vocabulary 64) on a copy task
+    under the masked-diffusion objective in float32 on the GPU; twelve fresh prompts are
+    decoded by the Flash-Cache + Flash-Verify loop (block 32, gamma 0.9, three batch rows,
+    refills) with the bf16 model on the HIP kernels and with the float32 model on the unfused
+    torch driver, and compared position by position (fdl.copy_task.compare_decodes)."""
+    import torch
+    from flash_cache_hip import flash_fused_elastic_cache
+    from fdl.copy_task import (CONFIG, GEN_LEN, N_TOKENS, PROMPT_LEN, compare_decodes,
+                               train_copy_model)
+    from fdl.generate import DecodeStats, generate_with_Flash_dLLM
+    from fdl.model import LLaDAConfig, build_model
+    from fdl.torch_path import flash_fused_elastic_cache_torch
+
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    twin, acc, gap = train_copy_model(dev, flash_fused_elastic_cache_torch)
+    train_s = time.time() - t0
+    hip = build_model(LLaDAConfig(**CONFIG), flash_fused_elastic_cache, dev, torch.bfloat16)
+    hip.load_state_dict({k: v.to(torch.bfloat16) for k, v in twin.state_dict().items()})
+    rng = np.random.default_rng(11)
+    n = 12
+    prompts = [torch.from_numpy(rng.integers(0, N_TOKENS, PROMPT_LEN)) for _ in range(n)]
+    cases = []
+    for verify, threshold in ((False, 0.9), (False, 1.01), (True, 1.01)):
+        kw = dict(gen_length=GEN_LEN, block_length=32, mask_id=63, eos_id=62,
+                  threshold=threshold, gamma=0.9, track_num=1, mask_num=1, verify=verify)
+        st = DecodeStats()
+        r_h, _, _ = generate_with_Flash_dLLM(hip, prompts, [PROMPT_LEN] * n, 3, [None] * n,
+                                             [0] * n, stats=st, device_schedule=True, **kw)
+        r_t, _, _ = generate_with_Flash_dLLM(twin, prompts, [PROMPT_LEN] * n, 3, [None] * n,
+                                             [0] * n, use_gpu_rank=False, **kw)
+        c = compare_decodes(prompts, r_h, r_t)
+        cases.append({"verify": verify, "threshold": threshold, "positions": c["positions"],
+                      "agreement": round(c["agreement"], 4), "right": round(c["right"], 4),
+                      "responses_of_different_length": c["content_mismatch"],
+                      "steps": st.steps, "verify_accepted": st.verify_accepted})
+    del hip, twin
+    torch.cuda.empty_cache()
+    return {"model": "2 layers, d_model 256, 2 heads x 128, SiLU MLP 512, vocab 64, trained "
+                     "on a copy task (prompt 32 tokens, response = prompt twice, then EOS)",
+            "train": {"accuracy_masked_tokens": round(acc, 4),
+                      "smallest_top2_logit_gap": round(gap, 2), "seconds": round(train_s, 1)},
+            "compared": "HIP bf16 decode (device schedule) against the float32 model on the "
+                        "unfused driver, every position decoded by both",
+            "cases": cases,
+            "agreement_all_positions": round(min(c["agreement"] for c in cases), 4)}
 
 
 def run_cpu_e2e_step(model_gpu, tokens_per_step: float, seed: int = 0) -> dict:
