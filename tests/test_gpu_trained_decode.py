@@ -38,19 +38,29 @@ def models():
 # threshold 0.9: the trained model passes it with every masked token, so a block decodes in
 # one step; 1.01: pass 1 keeps one token per step (keep = max(#conf >= threshold, 1)), so
 # the decode runs a step per token with tracked refreshes, and Flash-Verify accepts drafts
-@pytest.mark.parametrize("verify,device_schedule,threshold,kv_pages", [
-    (False, False, 0.9, None), (False, False, 1.01, None), (True, False, 1.01, None),
-    (True, True, 1.01, None), (True, True, 1.01, 12)])
+# (verify, device_schedule, threshold, kv_pages, block_length, track_num, mask_num)
+CASES = [
+    (False, False, 0.9, None, 32, 1, 1), (False, False, 1.01, None, 32, 1, 1),
+    (True, False, 1.01, None, 32, 1, 1), (True, True, 1.01, None, 32, 1, 1),
+    (True, True, 1.01, 12, 32, 1, 1),
+    # other block lengths (verify needs a prompt of 2 blocks: not at block 64), and more
+    # tracked / look-ahead blocks
+    (True, True, 1.01, None, 16, 1, 1), (False, False, 1.01, None, 64, 1, 1),
+    (False, True, 1.01, None, 16, 2, 2), (True, True, 1.01, None, 16, -1, 2),
+]
+
+
+@pytest.mark.parametrize("verify,device_schedule,threshold,kv_pages,block,track,mask", CASES)
 def test_trained_model_greedy_decode_matches_float32(models, verify, device_schedule, threshold,
-                                                     kv_pages):
+                                                     kv_pages, block, track, mask):
     """Twelve fresh prompts, three batch rows (refills); every decoded position of the HIP
     bf16 decode equals the float32 decode's, and both copy the prompt."""
     hip, twin = models
     rng = np.random.default_rng(11)
     n = 12
     prompts = [torch.from_numpy(rng.integers(0, N_TOKENS, PROMPT_LEN)) for _ in range(n)]
-    kw = dict(gen_length=GEN_LEN, block_length=32, mask_id=63, eos_id=62, threshold=threshold,
-              gamma=0.9, track_num=1, mask_num=1, verify=verify)
+    kw = dict(gen_length=GEN_LEN, block_length=block, mask_id=63, eos_id=62,
+              threshold=threshold, gamma=0.9, track_num=track, mask_num=mask, verify=verify)
     st_h, st_t = DecodeStats(), DecodeStats()
     r_h, _, _ = generate_with_Flash_dLLM(hip, prompts, [PROMPT_LEN] * n, 3, [None] * n, [0] * n,
                                          stats=st_h, device_schedule=device_schedule,
@@ -59,8 +69,8 @@ def test_trained_model_greedy_decode_matches_float32(models, verify, device_sche
                                          [0] * n, stats=st_t, use_gpu_rank=False, **kw)
     c = compare_decodes(prompts, r_h, r_t)
     print(f"verify={verify} device_schedule={device_schedule} threshold={threshold} "
-          f"kv_pages={kv_pages}: {c}; steps {st_h.steps} (float32 {st_t.steps}), verify "
-          f"accepted {st_h.verify_accepted}")
+          f"kv_pages={kv_pages} block={block} track={track} mask={mask}: {c}; steps "
+          f"{st_h.steps} (float32 {st_t.steps}), verify accepted {st_h.verify_accepted}")
     assert c["content_mismatch"] == 0
     assert c["positions"] >= n * GEN_LEN
     assert c["agreement"] >= 0.99
