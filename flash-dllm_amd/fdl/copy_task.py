@@ -104,8 +104,8 @@ def compare_decodes(prompts, resp_a, resp_b) -> dict:
     equally confident rows each step takes); `right` counts decode a's tokens equal to the
     task's answer."""
     pos = same = right = tails = content_mismatch = 0
-    for p, a, b in zip(prompts, resp_a, resp_b):
-        a, b = list(a), list(b)
+    for i, p in enumerate(prompts):
+        a, b = list(resp_a[i]), list(resp_b[i])  # lists, or dicts by prompt index
         ea = a.index(EOS) if EOS in a else len(a)
         eb = b.index(EOS) if EOS in b else len(b)
         content_mismatch += int(ea != eb)

@@ -77,3 +77,37 @@ def test_trained_model_greedy_decode_matches_float32(models, verify, device_sche
     assert c["right"] >= 0.99
     if verify:
         assert st_h.verify_accepted > 0  # drafts of a confident model pass gamma
+
+
+@pytest.mark.parametrize("verify", [False, True])
+def test_trained_model_reference_loop_through_hip_driver(models, verify):
+    """The reference's decode loop, restated statement for statement
+    (oracle/generate_oracle.py; info = [], int64 block tables, the dense verify mask), driving
+    the HIP drop-in driver on the trained model: the same tokens, token counts and
+    per-prompt step counts as the product loop (fdl.generate) on the same kernels, with
+    refills (six prompts, three rows) and, with Flash-Verify, accepted drafts; and the task's
+    answer."""
+    from oracle.generate_oracle import generate_oracle
+    hip, _ = models
+    rng = np.random.default_rng(3)
+    n = 6
+    prompts = [torch.from_numpy(rng.integers(0, N_TOKENS, PROMPT_LEN)) for _ in range(n)]
+    kw = dict(gen_length=GEN_LEN, block_length=32, mask_id=63, threshold=1.01, gamma=0.9,
+              track_num=1, mask_num=1, verify=verify)
+    steps_o = [0] * n
+    resp_o, nt_o, mx_o = generate_oracle(hip, prompts, [PROMPT_LEN] * n, 3, steps_o, eos_id=62,
+                                         **kw)
+    steps_p = [0] * n
+    st = DecodeStats()
+    resp_p, nt_p, mx_p = generate_with_Flash_dLLM(hip, prompts, [PROMPT_LEN] * n, 3, [None] * n,
+                                                  steps_p, eos_id=62, use_gpu_rank=False,
+                                                  stats=st, **kw)
+    print(f"verify={verify}: steps {steps_o} / {steps_p}, tokens {nt_o} / {nt_p}, verify "
+          f"accepted {st.verify_accepted}")
+    assert steps_p == steps_o and (nt_p, mx_p) == (nt_o, mx_o)
+    for i in range(n):
+        assert resp_p[i] == resp_o[i], i
+    c = compare_decodes(prompts, resp_p, resp_o)
+    assert c["right"] >= 0.99
+    if verify:
+        assert st.verify_accepted > 0
