@@ -339,6 +339,87 @@ def test_block_attention_softmax_importance_store_and_two_pass():
     _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="softmax importance")
 
 
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM])
+def test_block_attention_short_key_ranges(imp_mode):
+    """Key ranges at the edges of the LDS ring (three 64-key stages, two of them requested
+    before the first block is handed over): 1 to 191 keys, in 64-row tiles (with 32
+    importance rows: probabilities kept on chip; with 48: the second pass over K, whose
+    blocks may all still be resident) and in 128-row tiles, against the oracle."""
+    B, L, H = 8, 256, 4
+    k_ends = [1, 40, 64, 65, 127, 129, 191, 192]
+    n_q = [3, 40, 64, 60, 100, 120, 64, 90]
+    n_imp = [1, 32, 48, 32, 48, 32, 48, 32]
+    seqs, blocks, mb, q0 = [], [], [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q[b]),
+                            n_imp=n_imp[b] if imp_mode else 0))
+        blocks.append((b, k_ends[b], q0, q0 + n_q[b]))
+        mb.append((b, k_ends[b], q0, q0 + n_imp[b]))
+        q0 += n_q[b]
+    Q = q0
+    q, kc, vc = _attn_inputs(21, Q, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    assert plan.n_long == 0 and plan.n_mid == 3
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV) if imp_mode else None
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode, imp)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    _close(_np(out), orc.block_attention(qn, kn, vn, np.array(blocks), L, H, scale),
+           what="attention out")
+    if imp_mode:
+        bm = max(n_imp)  # the raw mode's mean over block_m rows and heads
+        scores = torch.zeros(B * L, dtype=torch.float32, device=DEV)
+        ops.importance_accumulate(imp, plan, 1.0 / (bm * H) if imp_mode == lib.IMP_RAW_LOGIT
+                                  else 1.0, scores)
+        torch.cuda.synchronize()
+        if imp_mode == lib.IMP_RAW_LOGIT:
+            exp = orc.importance_accumulate(np.zeros(B * L, np.float32),
+                                            orc.importance_raw_S(qn, kn, np.array(mb), B, L, H, bm))
+        else:
+            exp = orc.importance_softmax_colsum(qn, kn, np.array(mb), B, L, H, scale)
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="importance")
+
+
+@pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT])
+def test_block_attention_long_tiles_few_key_blocks(imp_mode):
+    """256-row tiles over one to three key blocks (the two-group kernel requests two blocks
+    before the first hand-over and the third after it): 200 rows over 40, 64, 100, 128 and
+    170 keys, against the oracle."""
+    B, L, H = 5, 256, 2
+    k_ends = [40, 64, 100, 128, 170]
+    n_q = 200
+    seqs, blocks, mb, q0 = [], [], [], 0
+    for b in range(B):
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=np.arange(q0, q0 + n_q),
+                            n_imp=32 if imp_mode else 0))
+        blocks.append((b, k_ends[b], q0, q0 + n_q))
+        mb.append((b, k_ends[b], q0, q0 + 32))
+        q0 += n_q
+    Q = q0
+    q, kc, vc = _attn_inputs(22, Q, B * L, H)
+    plan = make_plan(seqs, contiguous_page_table(B, L), device=DEV)
+    plan.validate(Q, B * L)
+    assert plan.n_long == B
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, B * L), dtype=torch.float32, device=DEV) if imp_mode else None
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode, imp)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    _close(_np(out), orc.block_attention(qn, kn, vn, np.array(blocks), L, H, scale),
+           what="attention out")
+    if imp_mode:
+        scores = torch.zeros(B * L, dtype=torch.float32, device=DEV)
+        ops.importance_accumulate(imp, plan, 1.0 / (32 * H), scores)
+        torch.cuda.synchronize()
+        exp = orc.importance_accumulate(np.zeros(B * L, np.float32),
+                                        orc.importance_raw_S(qn, kn, np.array(mb), B, L, H, 32))
+        _close(scores.cpu().numpy(), exp, atol=1e-3, rtol=1e-3, what="raw importance")
+
+
 @pytest.mark.parametrize("imp_mode", [lib.IMP_NONE, lib.IMP_RAW_LOGIT])
 def test_block_attention_key_ranges_beyond_the_staged_slot_map(imp_mode):
     """Key ranges longer than the 2048 keys whose slots a workgroup stages in LDS (slots then
