@@ -927,9 +927,10 @@ def run_e2e_agreement(model, prompts, lengths, kw, tf_steps: int, free_steps: in
         "free_running": {
             "steps": free_steps, "positions_decoded_by_both": int(both.sum()),
             "agreement": round(float(same.mean()), 4) if same.size else None},
-        "north_star_bar": ">= 99% of positions; met on decisive rows, not on all rows (near-tied "
-                          "logits of random weights flip under any bf16 arithmetic); on all "
-                          "positions for a trained model (greedy_agreement_trained)"}
+        "criterion": ">= 99% of positions identical under greedy decoding; met on decisive "
+                     "rows, not on all rows (near-tied logits of random weights flip under any "
+                     "bf16 arithmetic); on all positions for a trained model "
+                     "(greedy_agreement_trained)"}
 
 
 def run_trained_agreement() -> dict:
