@@ -1159,7 +1159,7 @@ def main() -> int:
                          "profiles")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+        print(f"bench.py measures one GPU only (there is no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
     if args.kernel:

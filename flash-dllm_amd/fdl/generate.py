@@ -1,4 +1,4 @@
-"""Decode scheduler of Flash-dLLM (Flash-Cache + Flash-Verify), restated for this build.
+"""Decode scheduler of Flash-dLLM (Flash-Cache + Flash-Verify), restated over the HIP kernels.
 
 `generate_with_Flash_dLLM` keeps the reference's signature and decisions
 (llada/generate.py:61-472):
@@ -160,8 +160,8 @@ def _to_dev_many(arrays: list, device) -> list:
 
 
 def _accepts_logit_rows(model) -> bool:
-    """True if model.forward takes a `logit_rows` argument (this build's model does; the
-    reference's LLaDAModelLM does not)."""
+    """True if model.forward takes a `logit_rows` argument (fdl.model's LLaDAModelLM does; the
+    reference's does not)."""
     try:
         params = inspect.signature(model.forward).parameters
     except (TypeError, ValueError):

@@ -6,8 +6,8 @@ F.linear Q/K/V, rotate-half RoPE on gathered sin/cos rows, index_copy_ into the 
 per-block softmax attention in float32 (probabilities cast to bf16 before PV, like
 flash_cache_triton.py:168), the raw-logit importance `attn_scores += S.mean((0, 1))`, the
 verify attention over gathered cache keys plus in-block keys under the mask, and the
-block's norm/MLP tail with the model's own modules. Every op is a PyTorch op: no HIP kernel
-of this build runs here. It is selected explicitly (model.set_attention); nothing falls
+block's norm/MLP tail with the model's own modules. Every op is a PyTorch op: no kernel of
+libfdl.so runs here. It is selected explicitly (model.set_attention); nothing falls
 back to it.
 """
 from __future__ import annotations

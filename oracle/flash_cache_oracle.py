@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. This module is the oracle that the HIP kernels are checked
 against. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-it, and only as the checker or as the timed CPU baseline; the product path (the
+it, and only to check results or as the timed CPU baseline; the product path (the
 flash-dllm_amd package) never imports or calls it.
 
 Each function restates one piece of the reference and cites the file:line it follows
