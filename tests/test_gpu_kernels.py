@@ -821,3 +821,61 @@ def test_verify_end_to_end_projection_and_attention():
     _close(_np(q), q_ref, what="verify Q")
     _close(_np(k1), k_ref, what="verify K")
     _close(_np(out), ref, what="verify attention")
+
+
+@pytest.mark.parametrize("page_log2", [4, 7, 12])
+def test_block_attention_page_sizes(page_log2):
+    """Page sizes 16, 128 and 4096 slots (the ABI's range is 16-4096) in randomly permuted
+    tables, cache lengths that are not multiples of the page size, every tile class (64-row,
+    128-row, 256-row full recomputes) and key ranges past the staged slot map (2100 keys in
+    a 64-row tile, 2200 in a full recompute: slots looked up from the page table in the
+    loop), raw importance; against the oracle through the same page table, rows outside the
+    tiles untouched."""
+    P = 1 << page_log2
+    rng = np.random.default_rng(40 + page_log2)
+    H = 4
+    k_ends = [300, 777, 1100, 2200, 517, 2100]
+    q_lens = [40, 100, 1100, 2200, 517, 50]  # 64-row, 128-row, full, full, full, 64-row
+    B = len(k_ends)
+    max_pages = (max(k_ends) + P - 1) // P
+    n_pages = sum((k + P - 1) // P for k in k_ends) + 3
+    perm = rng.permutation(n_pages)
+    table = np.zeros((B, max_pages), np.int32)
+    nxt = 0
+    for b in range(B):
+        for p in range((k_ends[b] + P - 1) // P):
+            table[b, p] = perm[nxt]
+            nxt += 1
+    seqs, row = [], 2  # rows 0 and 1 belong to no tile
+    for b in range(B):
+        rows = np.arange(row, row + q_lens[b])
+        seqs.append(SeqRows(batch=b, k_end=k_ends[b], rows=rows, n_imp=min(q_lens[b], 32)))
+        row += q_lens[b]
+    Q = row
+    n_slots = n_pages * P
+    q, kc, vc = _attn_inputs(41 + page_log2, Q, n_slots, H)
+    plan = make_plan(seqs, table, page_log2, device=DEV)
+    plan.validate(Q, n_slots)
+    assert plan.n_long > 0 and plan.n_mid > 0 and plan.n_work > plan.n_long + plan.n_mid
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, n_slots), dtype=torch.float32, device=DEV)
+    scores = torch.zeros(n_slots, dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale,
+                        lib.IMP_RAW_LOGIT, imp)
+    ops.importance_accumulate(imp, plan, 1.0, scores)
+    torch.cuda.synchronize()
+    qn, kn, vn = _np(q), _np(kc), _np(vc)
+    got = _np(out)
+    assert (got[:2] == POISON).all()
+    sc = scores.cpu().numpy()
+    for sq in seqs:
+        blk = np.array([[sq.batch, sq.k_end, sq.rows[0], sq.rows[-1] + 1]])
+        ref = orc.block_attention(qn, kn, vn, blk, 0, H, scale, page_table=table, page_size=P)
+        _close(got[sq.rows], ref[sq.rows], what=f"page {P}, seq {sq.batch}")
+        keys = orc.key_slots(sq.batch, sq.k_end, 0, table, P)
+        exp = np.zeros(len(keys))
+        for h in range(H):
+            cols = slice(h * 128, (h + 1) * 128)
+            exp += (qn[sq.rows[:sq.n_imp]][:, cols] @ kn[keys][:, cols].T).sum(0)
+        _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"page {P}, importance seq {sq.batch}")
