@@ -879,3 +879,20 @@ def test_block_attention_page_sizes(page_log2):
             cols = slice(h * 128, (h + 1) * 128)
             exp += (qn[sq.rows[:sq.n_imp]][:, cols] @ kn[keys][:, cols].T).sum(0)
         _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"page {P}, importance seq {sq.batch}")
+
+
+@pytest.mark.parametrize("n_heads,Q", [(6, 40), (6, 300), (20, 64), (20, 700), (40, 40),
+                                       (40, 200)])
+def test_qkv_rope_cache_head_counts(n_heads, Q):
+    """Head counts 6, 20 and 40 (d_model 768-5120): tile counts that are not multiples of
+    the eight XCDs (6 heads: 36 weight-streaming tiles) and the three launch shapes, against
+    the oracle; untouched cache rows keep their contents."""
+    rng = np.random.default_rng(100 + n_heads + Q)
+    n_slots = max(1024, 2 * Q)
+    slots = rng.choice(n_slots, Q, replace=False)
+    q, kc, vc, q_ref, k_ref, v_ref, s = _qkv_case(200 + Q, n_heads, Q, n_slots, slots)
+    _close(_np(q), q_ref, what="Q")
+    _close(_np(kc)[s], k_ref[s], what="K rows")
+    _close(_np(vc)[s], v_ref[s], what="V rows")
+    untouched = np.setdiff1d(np.arange(n_slots), s)
+    assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
