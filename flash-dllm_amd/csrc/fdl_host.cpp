@@ -34,6 +34,9 @@ extern "C" int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, i
                                  int64_t n_kv_rows, int64_t n_rope_rows, int32_t kv_packed) {
   FDL_REQUIRE(n_rows >= 0, FDL_ERR_SHAPE, "fdl_validate_rows: n_rows = %lld < 0",
               (long long)n_rows);
+  FDL_REQUIRE(n_kv_rows >= 0 && n_rope_rows >= 0, FDL_ERR_SHAPE,
+              "fdl_validate_rows: n_kv_rows = %lld, n_rope_rows = %lld (negative)",
+              (long long)n_kv_rows, (long long)n_rope_rows);
   if (n_rows == 0) return fdl::ok();
   FDL_REQUIRE_PTR(slot);
   if (kv_packed) {
@@ -41,7 +44,14 @@ extern "C" int fdl_validate_rows(const int64_t* slot, const int64_t* rope_row, i
                 "fdl_validate_rows: packed K/V needs n_kv_rows (%lld) == n_rows (%lld)",
                 (long long)n_kv_rows, (long long)n_rows);
   }
-  std::vector<uint8_t> seen(kv_packed ? 0 : static_cast<size_t>(n_kv_rows), 0);
+  // one byte per cache row for the duplicate check (no exception may leave the C ABI)
+  std::vector<uint8_t> seen;
+  try {
+    seen.assign(kv_packed ? 0 : static_cast<size_t>(n_kv_rows), 0);
+  } catch (...) {
+    return fdl::fail(FDL_ERR_SHAPE, "fdl_validate_rows: n_kv_rows = %lld is too large to check",
+                     (long long)n_kv_rows);
+  }
   for (int64_t r = 0; r < n_rows; ++r) {
     const int64_t s = slot[r];
     const int64_t rr = rope_row ? rope_row[r] : s;
@@ -72,7 +82,13 @@ extern "C" int fdl_validate_work(const int32_t* work, int64_t n_work, const int3
   FDL_REQUIRE(page_log2 >= 4 && page_log2 <= 12, FDL_ERR_SHAPE,
               "fdl_validate_work: page_log2 = %d outside [4, 12]", page_log2);
   const int64_t page = int64_t(1) << page_log2;
-  std::vector<int32_t> imp_tiles(static_cast<size_t>(n_seq > 0 ? n_seq : 0), 0);
+  std::vector<int32_t> imp_tiles;  // importance tiles per sequence
+  try {
+    imp_tiles.assign(static_cast<size_t>(n_seq > 0 ? n_seq : 0), 0);
+  } catch (...) {
+    return fdl::fail(FDL_ERR_SHAPE, "fdl_validate_work: n_seq = %lld is too large to check",
+                     (long long)n_seq);
+  }
   for (int64_t w = 0; w < n_work; ++w) {
     const int32_t* it = work + 8 * w;
     const int32_t b = it[0], kb = it[1], ke = it[2], roff = it[3], nr = it[4], ni = it[5];

@@ -160,6 +160,10 @@ def test_validate_rows():
     assert "rope row 9" in _expect(lib.FDL_ERR_RANGE, "fdl_validate_rows", sp, rp, 3, 8, 8, 0)
     # packed K/V: duplicate slots are fine (nothing is scattered), rope rows still checked
     lib.call("fdl_validate_rows", dp, None, 3, 3, 8, 1)
+    # sizes that cannot be checked come back as errors, not as a terminated process
+    assert "negative" in _expect(lib.FDL_ERR_SHAPE, "fdl_validate_rows", sp, None, 3, -1, 8, 0)
+    assert "too large" in _expect(lib.FDL_ERR_SHAPE, "fdl_validate_rows", sp, None, 3,
+                                  1 << 62, 8, 0)
 
 
 def test_build_work_tile_classes():
