@@ -247,3 +247,28 @@ def test_page_placement_invariance_full_size():
     assert torch.equal(out1, out2)
     assert torch.equal(imp2[:, mv], imp1)
     assert imp1.abs().sum() > 0
+
+
+def test_row_order_invariance_full_size():
+    """The block-table stress batch at full size without importance, each sequence's query
+    rows listed in a shuffled order: rows land in other tiles, wavefronts and lanes (and
+    other 256-row tiles of the full recomputes), and every output row is bit-identical,
+    since a row's attention is computed over the same keys in the same order wherever it
+    sits."""
+    import bench
+    st = bench.build_stress(seed=9)
+    P, n_slots, Q = st["P"], st["n_slots"], st["Q"]
+    rng = np.random.default_rng(91)
+    gen = torch.Generator().manual_seed(92)
+    q = _bf(gen, Q, D).to(DEV)
+    kc, vc = st["kc"].to(DEV), st["vc"].to(DEV)
+    shuffled = [SeqRows(batch=s.batch, k_end=s.k_end, rows=rng.permutation(s.rows), n_imp=0)
+                for s in st["seqs"]]
+    outs = []
+    for seqs in (st["seqs"], shuffled):
+        plan = make_plan(seqs, st["table"], 5, device=DEV)
+        out = torch.empty((Q, D), dtype=torch.bfloat16, device=DEV)
+        ops.block_attention(q, kc, vc, plan, out, H, 1.0 / np.sqrt(HD))
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
