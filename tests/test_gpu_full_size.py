@@ -272,3 +272,34 @@ def test_row_order_invariance_full_size():
         outs.append(out)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
+
+
+def test_verify_block_order_invariance_full_size():
+    """The Flash-Verify batch at full size (16 blocks x 32 heads: two heads per workgroup),
+    its packed projection, then the verify attention with the closed-form masks over the
+    blocks listed forward and reversed: every block's rows are bit-identical (a block's
+    rows attend to its own key list and in-block keys in the same order either way)."""
+    import bench
+    vf = bench.build_verify(seed=11)
+    Q = vf["Q"]
+    x = vf["x"].to(DEV)
+    w = [t.to(DEV) for t in vf["w"]]
+    sin, cos = vf["sin"].to(DEV), vf["cos"].to(DEV)
+    q, k1, v1 = (torch.empty((Q, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    ops.qkv_rope_cache(x, *w, sin, cos, torch.from_numpy(vf["slots"]).to(DEV), q, k1, v1, H,
+                       kv_packed=True)
+    kc, vc = vf["kc"].to(DEV), vf["vc"].to(DEV)
+    kp = torch.from_numpy(vf["key_pos"]).to(DEV)
+    ts = np.array([[0, int(s)] for s in vf["kv"]], np.int32)  # T = 0 fill rows, S candidates
+    rows = 2 * vf["BMV"]
+    outs = []
+    for order in (np.arange(vf["NV"]), np.arange(vf["NV"])[::-1]):
+        vb = torch.from_numpy(np.ascontiguousarray(vf["vblocks"][order])).to(DEV)
+        tsd = torch.from_numpy(np.ascontiguousarray(ts[order])).to(DEV)
+        out = torch.full((Q, D), 7.0, dtype=torch.bfloat16, device=DEV)
+        ops.verify_attention(q, k1, v1, kc, vc, kp, vb, tsd, rows, out, H, 1.0 / np.sqrt(HD))
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert vf["NV"] * H > 256
+    assert torch.equal(outs[0], outs[1])
+    assert not (outs[0] == 7.0).all(dim=1).any()  # every row written
