@@ -426,3 +426,34 @@ def test_device_schedule_matches_host_schedule(verify, block, lengths):
     assert r_d == r_h and n_d == n_h and m_d == m_h and s_d == s_h
     assert st_d.steps == st_h.steps and st_d.decoded == st_h.decoded
     assert st_d.host_syncs <= st_d.steps + 1 + 5
+
+
+@pytest.mark.parametrize("verify", [False, True])
+def test_device_schedule_matches_host_schedule_eval_preset(verify):
+    """The reference's evaluation preset's batch shape (llada/eval_gsm8k.sh:7-15: 32 batch
+    rows, block 16): 40 prompts of 48-140 tokens through 32 rows (refills), the device
+    schedule against the host schedule, token for token, with the same per-prompt step
+    counts; both Flash-Cache only and with Flash-Verify."""
+    model = _model(lm_head_std=1.0, seed=4)
+    rng = np.random.default_rng(21)
+    n = 40
+    lengths = [int(v) for v in rng.integers(48, 141, n)]
+    prompts = [torch.from_numpy(rng.integers(0, 2000, m)) for m in lengths]
+    kw = dict(gen_length=48, block_length=16, mask_id=2046, threshold=0.9, gamma=0.9,
+              track_num=1, mask_num=1, eos_id=2045, verify=verify)
+    out = []
+    for device_schedule in (False, True):
+        st = DecodeStats()
+        steps = [0] * n
+        r, nt, mx = generate_with_Flash_dLLM(model, prompts, lengths, 32, [None] * n, steps,
+                                             stats=st, device_schedule=device_schedule, **kw)
+        out.append((r, nt, mx, steps, st))
+    (r_h, n_h, m_h, s_h, st_h), (r_d, n_d, m_d, s_d, st_d) = out
+    print(f"verify={verify}: {st_d.steps} steps, {st_d.host_syncs} host syncs (device), "
+          f"decoded {st_d.decoded}, verify accepted {st_d.verify_accepted}")
+    assert r_d == r_h and n_d == n_h and m_d == m_h and s_d == s_h
+    assert st_d.steps == st_h.steps and st_d.decoded == st_h.decoded
+    assert st_d.host_syncs <= st_d.steps + 1 + n
+    assert st_d.steps > 3 * n // 32 and st_d.decoded >= n * 16
+    if verify:
+        assert st_d.verify_accepted > 0
