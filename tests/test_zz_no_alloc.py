@@ -1,7 +1,8 @@
 """fdl_block_attention_scores_noalloc (the entry point that allocates nothing) against
 fdl_block_attention + fdl_importance_accumulate with a caller workspace, through the C ABI:
 attention output and scores bit for bit, on two calls in a row, the second one smaller
-(the library's static scratch keeps the first call's partials)."""
+(the library's static scratch keeps the first call's partials); and captured in a HIP graph,
+every replay equal to the eager call."""
 import numpy as np
 import pytest
 import torch
@@ -112,3 +113,52 @@ def test_noalloc_rejects_partials_beyond_the_scratch():
                  None, 1, 1, 5, None, 1, None, 1, 64, 0.1, None, lib.IMP_RAW_LOGIT, 1.0, None, None)
     assert ei.value.status == lib.FDL_ERR_UNSUPPORTED
     assert "scratch" in str(ei.value)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("imp_mode", [lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM])
+def test_noalloc_captured_in_a_graph(imp_mode):
+    """The allocation-free entry point as its callers use it: captured in a HIP graph (every
+    tile class of the 5-sequence case), replayed four times with the scores reset and the
+    output poisoned by eager work between the replays; every replay equals the eager call."""
+    q, kc, vc, plan, scores0, H = _case(23, 5, [300, 700, 900, 513, 128],
+                                        [300, 100, 64, 40, 1], 32)
+    n_slots, D = kc.shape[0], q.shape[1]
+    scale = 1.0 / np.sqrt(128)
+    imp_scale = 1.0 / (32 * H) if imp_mode == lib.IMP_RAW_LOGIT else 1.0
+    out = torch.empty_like(q)
+    sc = torch.empty_like(scores0)
+    n_idx = max(int(plan.row_idx.size), 1)
+
+    def call(stream):
+        for first, count, tile_rows in _classes(plan):
+            if count:
+                lib.call("fdl_block_attention_scores_noalloc", q.data_ptr(), kc.data_ptr(),
+                         vc.data_ptr(), q.shape[0], n_slots, D, H, 128,
+                         plan.page_table_d.data_ptr(), plan.page_table.shape[0],
+                         plan.page_table.shape[1], plan.page_log2,
+                         plan.work_d[first:].data_ptr(), count, plan.row_idx_d.data_ptr(), n_idx,
+                         tile_rows, scale, out.data_ptr(), imp_mode, imp_scale, sc.data_ptr(),
+                         stream)
+
+    def reset():
+        sc.copy_(scores0)
+        out.fill_(float("nan"))
+
+    reset()
+    call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = (out.clone(), sc.clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call(s.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        reset()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[0]), f"replay {rep}: output"
+        assert torch.equal(sc, eager[1]), f"replay {rep}: scores"
