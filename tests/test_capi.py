@@ -124,6 +124,32 @@ def test_launchers_reject_bad_scalars_without_gpu():
     lib.call("fdl_silu_mul", None, None, 0, None, None)
 
 
+def test_elementwise_launchers_reject_bad_arguments_without_gpu():
+    """RMSNorm and SiLU-gating: the width and count rules, eps, the residual / sum pairing and
+    NULL or misaligned buffers are refused on the host before any launch."""
+    buf = np.zeros(64, dtype=np.uint16)
+    p = buf.ctypes.data
+    assert p % 16 == 0
+    _expect(lib.FDL_ERR_SHAPE, "fdl_rms_norm", p, None, p, -1, 16, 1e-5, None, p, None)
+    for d in (0, 12, 8200):
+        _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_rms_norm", p, None, p, 2, d, 1e-5, None, p, None)
+    assert "eps" in _expect(lib.FDL_ERR_SHAPE, "fdl_rms_norm", p, None, p, 2, 16, -1.0, None, p,
+                            None)
+    for args in ((None, None, p), (p, None, None), (None, p, p)):
+        x, out, w = args
+        _expect(lib.FDL_ERR_NULL, "fdl_rms_norm", x, None, w, 2, 16, 1e-5, None, out, None)
+    msg = _expect(lib.FDL_ERR_NULL, "fdl_rms_norm", p, p, p, 2, 16, 1e-5, None, p, None)
+    assert "sum_out" in msg
+    msg = _expect(lib.FDL_ERR_SHAPE, "fdl_rms_norm", p + 2, None, p, 2, 16, 1e-5, None, p, None)
+    assert "aligned" in msg
+    _expect(lib.FDL_ERR_SHAPE, "fdl_rms_norm", p, p + 4, p, 2, 16, 1e-5, p, p, None)
+    for n in (-8, 12):
+        _expect(lib.FDL_ERR_UNSUPPORTED, "fdl_silu_mul", p, p, n, p, None)
+    for args in ((None, p, p), (p, None, p), (p, p, None)):
+        _expect(lib.FDL_ERR_NULL, "fdl_silu_mul", args[0], args[1], 16, args[2], None)
+    _expect(lib.FDL_ERR_SHAPE, "fdl_silu_mul", p, p, 16, p + 8, None)
+
+
 def test_gate_up_weights_share_one_buffer():
     """LLaDABlock lays ff_proj / up_proj out as one [2h, d] buffer (values kept), so the
     block epilogue can run them as one GEMM; separate buffers are detected."""
