@@ -896,3 +896,79 @@ def test_qkv_rope_cache_head_counts(n_heads, Q):
     _close(_np(vc)[s], v_ref[s], what="V rows")
     untouched = np.setdiff1d(np.arange(n_slots), s)
     assert np.all(_np(kc)[untouched] == POISON) and np.all(_np(vc)[untouched] == POISON)
+
+
+def _f64_attention(qr, keys_k, keys_v, scale):
+    s = (qr @ keys_k.T) * scale
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ keys_v, p
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_attention_random_plans(seed):
+    """Seeded random launches: 1-7 sequences with key ranges [k_begin, k_end), k_end up to
+    1300 (a quarter of them starting past 0), 1-200 query rows or a full recompute (q = k),
+    every sequence's rows scattered over the packed row space, pages of 16-256 slots
+    permuted over a pool, one, two or four heads, the three importance modes in turn. The
+    outputs against float64 softmax attention over each sequence's keys; the per-head
+    importance partials at every key slot (zero for sequences without importance rows and
+    for slots outside every key range)."""
+    rng = np.random.default_rng(1000 + seed)
+    imp_mode = (lib.IMP_NONE, lib.IMP_RAW_LOGIT, lib.IMP_SOFTMAX_COLSUM)[seed % 3]
+    H = int(rng.choice([1, 2, 4]))
+    page_log2 = int(rng.choice([4, 5, 6, 8]))
+    P = 1 << page_log2
+    B = int(rng.integers(1, 8))
+    specs = []
+    for _ in range(B):
+        k_end = int(rng.integers(1, 1301))
+        k_begin = int(rng.integers(0, k_end)) if rng.random() < 0.25 else 0
+        nq = k_end - k_begin if rng.random() < 0.2 else int(rng.integers(1, 201))
+        n_imp = 0 if imp_mode == lib.IMP_NONE else int(rng.integers(0, min(nq, 64) + 1))
+        specs.append((k_begin, k_end, nq, n_imp))
+    max_pages = (1300 + P - 1) // P
+    n_pages = sum((k + P - 1) // P for _, k, _, _ in specs) + 5
+    perm = rng.permutation(n_pages)
+    table = np.zeros((B, max_pages), np.int32)
+    nxt = 0
+    for b, (_, k_end, _, _) in enumerate(specs):
+        for p in range((k_end + P - 1) // P):
+            table[b, p] = perm[nxt]
+            nxt += 1
+    Q = sum(s[2] for s in specs)
+    row_perm = rng.permutation(Q)
+    seqs, off = [], 0
+    for b, (k_begin, k_end, nq, n_imp) in enumerate(specs):
+        seqs.append(SeqRows(batch=b, k_end=k_end, rows=row_perm[off:off + nq], n_imp=n_imp,
+                            k_begin=k_begin))
+        off += nq
+    n_slots = n_pages * P
+    q, kc, vc = _attn_inputs(2000 + seed, Q, n_slots, H)
+    plan = make_plan(seqs, table, page_log2, device=DEV)
+    plan.validate(Q, n_slots)
+    out = torch.full((Q, H * 128), POISON, dtype=torch.bfloat16, device=DEV)
+    imp = torch.zeros((H, n_slots), dtype=torch.float32, device=DEV)
+    scale = orc.softmax_scale(128)
+    print(f"seed {seed}: H {H}, page {P}, imp {imp_mode}, specs {specs}", flush=True)
+    ops.block_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), plan, out, H, scale, imp_mode,
+                        imp if imp_mode else None)
+    torch.cuda.synchronize()
+    qn, kn, vn = (_np(t).astype(np.float64) for t in (q, kc, vc))
+    got, gimp = _np(out), imp.cpu().numpy()
+    covered = np.zeros(n_slots, bool)
+    for b, sq in enumerate(seqs):
+        keys = orc.key_slots(b, sq.k_end, 0, table, P, k_begin=sq.k_begin)
+        covered[keys] = True
+        for h in range(H):
+            cols = slice(h * 128, (h + 1) * 128)
+            o, p = _f64_attention(qn[sq.rows][:, cols], kn[keys][:, cols], vn[keys][:, cols],
+                                  scale)
+            _close(got[sq.rows][:, cols], o, what=f"seq {b} head {h}")
+            if imp_mode == lib.IMP_RAW_LOGIT:
+                exp = (qn[sq.rows[:sq.n_imp]][:, cols] @ kn[keys][:, cols].T).sum(0)
+                _close(gimp[h, keys], exp, atol=5e-3, rtol=1e-4, what=f"raw imp seq {b} head {h}")
+            elif imp_mode == lib.IMP_SOFTMAX_COLSUM:
+                exp = p[:sq.n_imp].sum(0)
+                _close(gimp[h, keys], exp, atol=1e-3, rtol=1e-3, what=f"softmax imp seq {b} head {h}")
+    assert not gimp[:, ~covered].any()
