@@ -59,6 +59,7 @@ struct QkvArgs {
   int n_mtiles;
   int n_tiles;
   int kv_packed;
+  int rope_half;  // sin/cos rows repeat their first half: read only that half
 };
 
 // LDS tile layout: chunk c (16 B) of tile row r is stored at chunk c ^ ((r >> 1) & 7) of
@@ -132,9 +133,14 @@ struct EpGroup {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         s1[h] = *reinterpret_cast<const f32x4*>(sn + 4 * h);
-        s2[h] = *reinterpret_cast<const f32x4*>(sn + kHalf + 4 * h);
         c1[h] = *reinterpret_cast<const f32x4*>(cs + 4 * h);
-        c2[h] = *reinterpret_cast<const f32x4*>(cs + kHalf + 4 * h);
+        if (a.rope_half) {
+          s2[h] = s1[h];
+          c2[h] = c1[h];
+        } else {
+          s2[h] = *reinterpret_cast<const f32x4*>(sn + kHalf + 4 * h);
+          c2[h] = *reinterpret_cast<const f32x4*>(cs + kHalf + 4 * h);
+        }
       }
     }
   }
@@ -487,7 +493,7 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
                                   int64_t n_rope_rows, const int64_t* slot,
                                   const int64_t* rope_row, int64_t n_rows, int64_t d_model,
                                   int64_t n_heads, int64_t head_dim, void* q_out, void* k_out,
-                                  void* v_out, int64_t n_kv_rows, int32_t kv_packed,
+                                  void* v_out, int64_t n_kv_rows, int32_t flags,
                                   void* stream) {
   using namespace fdl;
   FDL_REQUIRE(n_rows >= 0, FDL_ERR_SHAPE, "fdl_qkv_rope_cache: n_rows = %lld < 0",
@@ -503,8 +509,9 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   FDL_REQUIRE(d_model % kDAlign == 0, FDL_ERR_UNSUPPORTED,
               "fdl_qkv_rope_cache: d_model = %lld is not a multiple of %d", (long long)d_model,
               kDAlign);
-  FDL_REQUIRE(kv_packed == 0 || kv_packed == 1, FDL_ERR_SHAPE,
-              "fdl_qkv_rope_cache: kv_packed must be 0 or 1");
+  FDL_REQUIRE((flags & ~(FDL_QKV_KV_PACKED | FDL_QKV_ROPE_HALVES_EQUAL)) == 0, FDL_ERR_SHAPE,
+              "fdl_qkv_rope_cache: flags = %d has unknown bits", flags);
+  const int kv_packed = (flags & FDL_QKV_KV_PACKED) ? 1 : 0;
   FDL_REQUIRE(!kv_packed || n_kv_rows == n_rows, FDL_ERR_SHAPE,
               "fdl_qkv_rope_cache: packed K/V needs n_kv_rows == n_rows");
   FDL_REQUIRE(n_kv_rows >= 0 && n_rope_rows >= 0, FDL_ERR_SHAPE,
@@ -552,6 +559,7 @@ extern "C" int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk,
   args.n_mtiles = 0;
   args.n_tiles = 0;
   args.kv_packed = kv_packed;
+  args.rope_half = (flags & FDL_QKV_ROPE_HALVES_EQUAL) ? 1 : 0;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t tail = qkv_tail_rows(n_rows, 3 * n_heads * kHalf);
   const int64_t head = n_rows - tail;

@@ -24,7 +24,10 @@ FDL_ERR_RANGE = -3
 FDL_ERR_UNSUPPORTED = -4
 FDL_ERR_HIP = -5
 
-ABI_VERSION = 2  # FDL_ABI_VERSION of include/fdl.h
+ABI_VERSION = 3  # FDL_ABI_VERSION of include/fdl.h
+# fdl_qkv_rope_cache flags (FDL_QKV_KV_PACKED, FDL_QKV_ROPE_HALVES_EQUAL)
+QKV_KV_PACKED = 1
+QKV_ROPE_HALVES_EQUAL = 2
 # fp32 workspace per 64-key block, head and tile of softmax importance (FDL_ATTN_WS_FLOATS_PER_BLOCK)
 ATTN_WS_FLOATS_PER_BLOCK = 32 * 64 + 32
 # key blocks whose softmax-importance probabilities a tile keeps on chip (FDL_ATTN_ONCHIP_BLOCKS)
@@ -69,7 +72,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _p, _i64,            # rope_sin, rope_cos, n_rope_rows
         _p, _p, _i64,            # slot, rope_row, n_rows
         _i64, _i64, _i64,        # d_model, n_heads, head_dim
-        _p, _p, _p, _i64, _i32,  # q_out, k_out, v_out, n_kv_rows, kv_packed
+        _p, _p, _p, _i64, _i32,  # q_out, k_out, v_out, n_kv_rows, flags
         _p,                      # stream
     ]),
     "fdl_block_attention": (ctypes.c_int, [

@@ -7,6 +7,8 @@ a GPU is an error.
 """
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 
@@ -44,14 +46,47 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = Non
         raise _lib.FdlError(_lib.FDL_ERR_SHAPE, f"{name} must be contiguous")
 
 
+_halves_seen: dict = {}
+
+
+def tables_repeat_halves(rope_sin: torch.Tensor, rope_cos: torch.Tensor) -> bool:
+    """Whether every row of both RoPE tables repeats its first half (sin[r, c + hd/2] ==
+    sin[r, c], the same for cos), as tables built like the reference's cat(freqs, freqs)
+    (llada/generate.py:44-50) do. Compared on the device once per pair of table tensors (one
+    synchronisation) and remembered while both tensors live unmodified; under graph capture
+    an unseen pair counts as not repeating (nothing is compared)."""
+    key = (id(rope_sin), id(rope_cos))
+    hit = _halves_seen.get(key)
+    if (hit is not None and hit[0]() is rope_sin and hit[1]() is rope_cos
+            and hit[2] == (rope_sin._version, rope_cos._version)):
+        return hit[3]
+    if torch.cuda.is_current_stream_capturing():
+        return False
+    h = rope_sin.shape[1] // 2
+    same = bool(rope_sin.shape[1] % 2 == 0
+                and torch.equal(rope_sin[:, :h], rope_sin[:, h:])
+                and torch.equal(rope_cos[:, :h], rope_cos[:, h:]))
+    if len(_halves_seen) >= 64:
+        for k in [k for k, v in _halves_seen.items() if v[0]() is None or v[1]() is None]:
+            del _halves_seen[k]
+        if len(_halves_seen) >= 64:
+            _halves_seen.clear()
+    _halves_seen[key] = (weakref.ref(rope_sin), weakref.ref(rope_cos),
+                         (rope_sin._version, rope_cos._version), same)
+    return same
+
+
 def qkv_rope_cache(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor,
                    rope_sin: torch.Tensor, rope_cos: torch.Tensor, slot: torch.Tensor,
                    q_out: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor, n_heads: int,
-                   rope_row: torch.Tensor | None = None, kv_packed: bool = False) -> None:
+                   rope_row: torch.Tensor | None = None, kv_packed: bool = False,
+                   rope_halves_equal: bool | None = None) -> None:
     """Fused QKV projection + RoPE + K/V write (fdl_qkv_rope_cache).
 
     x [Q, D] bf16; w* [D, D] bf16; rope tables fp32 [R, hd]; slot int64 [Q];
     q_out [Q, D]; k_out/v_out the cache [n_slots, D] (or [Q, D] with kv_packed).
+    rope_halves_equal: whether every table row repeats its first half (then only that half
+    is read); None checks the tables once (see rope_halves_equal()).
     """
     dev = x.device
     _need(x, "x", BF16, 2)
@@ -81,11 +116,15 @@ def qkv_rope_cache(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torc
     _need(v_out, "v_out", BF16, 2, dev)
     if k_out.shape != v_out.shape or k_out.shape[1] != d_model:
         raise _lib.FdlError(_lib.FDL_ERR_SHAPE, "k_out/v_out must both be [n, d_model]")
+    if rope_halves_equal is None:
+        rope_halves_equal = tables_repeat_halves(rope_sin, rope_cos)
+    flags = (_lib.QKV_KV_PACKED if kv_packed else 0) | \
+        (_lib.QKV_ROPE_HALVES_EQUAL if rope_halves_equal else 0)
     _lib.call("fdl_qkv_rope_cache", x.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
               rope_sin.data_ptr(), rope_cos.data_ptr(), rope_sin.shape[0],
               slot.data_ptr(), _ptr(rope_row), n_rows, d_model, n_heads, head_dim,
               q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), k_out.shape[0],
-              1 if kv_packed else 0, _stream(x))
+              flags, _stream(x))
 
 
 def _class_ranges(plan: AttnPlan):

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FDL_ABI_VERSION 2
+#define FDL_ABI_VERSION 3
 
 enum fdl_status {
   FDL_OK = 0,
@@ -65,7 +65,7 @@ int fdl_abi_version(void);
 /*
  * Fused QKV projection + rotate-half RoPE + K/V write.
  * Replaces the launches of _flash_qkv_proj_cache_fwd (flash_cache_triton.py:15-100,
- * launched at :541-559) and, with kv_packed = 1, _flash_verify_qkv_proj_fwd
+ * launched at :541-559) and, with FDL_QKV_KV_PACKED, _flash_verify_qkv_proj_fwd
  * (flash_cache_triton.py:255-338, launched at :505-519).
  *
  *   x        bf16 [n_rows][d_model]         normalised hidden states (x_normed)
@@ -74,9 +74,13 @@ int fdl_abi_version(void);
  *   slot     int64 [n_rows]  cache slot of each row (the reference's query_pos_flat)
  *   rope_row int64 [n_rows]  row of the sin/cos tables for each row; NULL = use slot
  *   q_out    bf16 [n_rows][d_model]         rotated Q, packed by row
- *   k_out/v_out bf16: kv_packed == 0 -> cache [n_kv_rows][d_model], row slot[r] is
- *            overwritten with the rotated K / V of row r; kv_packed == 1 -> packed
+ *   k_out/v_out bf16: without FDL_QKV_KV_PACKED -> cache [n_kv_rows][d_model], row slot[r]
+ *            is overwritten with the rotated K / V of row r; with it -> packed
  *            [n_rows][d_model] (n_kv_rows must equal n_rows).
+ *   flags    FDL_QKV_KV_PACKED (1) and / or FDL_QKV_ROPE_HALVES_EQUAL (2): the caller
+ *            asserts that every sin/cos row repeats its first half (rope_sin[r][c + head_dim/2]
+ *            == rope_sin[r][c], the same for rope_cos), as the reference's tables do
+ *            (cat(freqs, freqs), generate.py:44-50); only the first half of each row is read.
  * Rows whose slot or rope_row is out of range are skipped by the kernel; use
  * fdl_validate_rows to reject them on the host. x, the weights, the sin/cos tables and the
  * outputs must be 16-byte aligned (d_model is a multiple of 256).
@@ -85,8 +89,9 @@ int fdl_qkv_rope_cache(const void* x, const void* wq, const void* wk, const void
                        const float* rope_sin, const float* rope_cos, int64_t n_rope_rows,
                        const int64_t* slot, const int64_t* rope_row, int64_t n_rows,
                        int64_t d_model, int64_t n_heads, int64_t head_dim, void* q_out,
-                       void* k_out, void* v_out, int64_t n_kv_rows, int32_t kv_packed,
+                       void* k_out, void* v_out, int64_t n_kv_rows, int32_t flags,
                        void* stream);
+enum { FDL_QKV_KV_PACKED = 1, FDL_QKV_ROPE_HALVES_EQUAL = 2 };
 
 /*
  * Block-table attention over the KV cache for variable per-sequence query lengths, with
@@ -225,7 +230,7 @@ int fdl_importance_accumulate_rank(const float* imp_part, int64_t n_heads, float
  * 341-428, launched at :523-535): for each verify block (k0, k1, q0, q1) and head, the
  * rows [q0, q1) attend to the cache keys key_slots[k0..k1) and to the block's own rows
  * as in-block keys (k_blk/v_blk, packed by row) under the block's boolean mask.
- *   q, k_blk, v_blk bf16 [n_q_rows][d_model]    (outputs of fdl_qkv_rope_cache, kv_packed=1)
+ *   q, k_blk, v_blk bf16 [n_q_rows][d_model]    (outputs of fdl_qkv_rope_cache, FDL_QKV_KV_PACKED)
  *   key_slots int64 [n_keys]
  *   vblocks  int32 [n_vblocks][4]; q1 - q0 <= block_rows <= 256 (the reference's 2 * block_m)
  *   exactly one of

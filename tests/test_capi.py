@@ -47,6 +47,12 @@ def test_launchers_reject_bad_scalars_without_gpu():
             10, None, None, 4, 4096, 32, 128, None, None, None, 10, 0, None)
     _expect(lib.FDL_ERR_SHAPE, "fdl_qkv_rope_cache", None, None, None, None, None, None,
             10, None, None, 4, 4096, 32, 128, None, None, None, 7, 1, None)
+    # flags: FDL_QKV_KV_PACKED (1) and FDL_QKV_ROPE_HALVES_EQUAL (2) only
+    assert "flags" in _expect(lib.FDL_ERR_SHAPE, "fdl_qkv_rope_cache", None, None, None, None,
+                              None, None, 10, None, None, 4, 4096, 32, 128, None, None, None,
+                              4, 4, None)
+    _expect(lib.FDL_ERR_NULL, "fdl_qkv_rope_cache", None, None, None, None, None, None,
+            10, None, None, 4, 4096, 32, 128, None, None, None, 4, 3, None)
     # zero rows is a no-op
     lib.call("fdl_qkv_rope_cache", None, None, None, None, None, None, 0, None, None, 0,
              4096, 32, 128, None, None, None, 0, 0, None)
@@ -302,3 +308,11 @@ def test_scheduler_record_fields_match_the_header():
     for name, value in fields.items():
         assert getattr(lib, name) == value, name
     assert re.search(r"FDL_SCHED_SEQ_FIELDS = (\d+)", hdr).group(1) == str(lib.SCHED_SEQ_FIELDS)
+
+
+def test_projection_flags_match_the_header():
+    hdr = HEADER.read_text()
+    assert re.search(r"FDL_QKV_KV_PACKED = (\d+)", hdr).group(1) == str(lib.QKV_KV_PACKED)
+    assert re.search(r"FDL_QKV_ROPE_HALVES_EQUAL = (\d+)", hdr).group(1) == str(
+        lib.QKV_ROPE_HALVES_EQUAL)
+    assert re.search(r"#define FDL_ABI_VERSION (\d+)", hdr).group(1) == str(lib.ABI_VERSION)

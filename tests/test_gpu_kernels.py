@@ -972,3 +972,44 @@ def test_block_attention_random_plans(seed):
                 exp = p[:sq.n_imp].sum(0)
                 _close(gimp[h, keys], exp, atol=1e-3, rtol=1e-3, what=f"softmax imp seq {b} head {h}")
     assert not gimp[:, ~covered].any()
+
+
+def test_qkv_rope_halves_flag():
+    """FDL_QKV_ROPE_HALVES_EQUAL. With the reference's tables (every row repeats its first
+    half) the projection that reads one half equals the one that reads both, bit for bit, and
+    the wrapper detects the repetition. Tables whose halves differ are detected as such and
+    projected with both halves (against the oracle); with the flag forced on them, the high
+    half's sin/cos are not read (the output changes)."""
+    H, Q, L = 4, 300, 512
+    gen = torch.Generator().manual_seed(41)
+    D = H * 128
+    x = _bf16((Q, D), gen)
+    w = [_bf16((D, D), gen, 0.02) for _ in range(3)]
+    slots = torch.from_numpy(np.random.default_rng(42).permutation(L)[:Q].astype(np.int64))
+    sin, cos = _rope(L)
+    assert ops.tables_repeat_halves(sin, cos)
+    xd, wd, sd = x.to(DEV), [t.to(DEV) for t in w], slots.to(DEV)
+
+    def run(s, c, flag):
+        q = torch.zeros((Q, D), dtype=torch.bfloat16, device=DEV)
+        kc = torch.full((L, D), POISON, dtype=torch.bfloat16, device=DEV)
+        vc = torch.full_like(kc, POISON)
+        ops.qkv_rope_cache(xd, *wd, s, c, sd, q, kc, vc, H, rope_halves_equal=flag)
+        torch.cuda.synchronize()
+        return q, kc, vc
+
+    both, half, auto = run(sin, cos, False), run(sin, cos, True), run(sin, cos, None)
+    for t0, t1, t2 in zip(both, half, auto):
+        assert torch.equal(t0, t1) and torch.equal(t0, t2)
+    ang = np.random.default_rng(43).uniform(-3.0, 3.0, (L, 128)).astype(np.float32)
+    s2, c2 = torch.from_numpy(np.sin(ang)).to(DEV), torch.from_numpy(np.cos(ang)).to(DEV)
+    assert not ops.tables_repeat_halves(s2, c2)
+    q, kc, vc = run(s2, c2, None)
+    poison = np.full((L, D), POISON, np.float32)
+    q_ref, k_ref, v_ref = orc.qkv_proj_cache(_np(x), _np(w[0]), _np(w[1]), _np(w[2]),
+                                             s2.cpu().numpy(), c2.cpu().numpy(), slots.numpy(),
+                                             H, poison, poison)
+    _close(_np(q), q_ref, what="q, halves differ")
+    _close(_np(kc), k_ref, what="k cache, halves differ")
+    _close(_np(vc), v_ref, what="v cache, halves differ")
+    assert not torch.equal(run(s2, c2, True)[0], q)
