@@ -182,6 +182,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Waits until at most n (clamped to 0 .. STAGES - 1) steps of kLoads loads each are in flight.
+template <int STAGES, int kLoads>
+__device__ __forceinline__ void wait_steps(int n) {
+  static_assert(STAGES >= 2 && STAGES <= 8, "stages");
+  switch (n <= 0 ? 0 : (n >= STAGES - 1 ? STAGES - 1 : n)) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<kLoads>(); break;
+    case 2: wait_vmcnt<(STAGES > 2 ? 2 : 0) * kLoads>(); break;
+    case 3: wait_vmcnt<(STAGES > 3 ? 3 : 0) * kLoads>(); break;
+    case 4: wait_vmcnt<(STAGES > 4 ? 4 : 0) * kLoads>(); break;
+    case 5: wait_vmcnt<(STAGES > 5 ? 5 : 0) * kLoads>(); break;
+    case 6: wait_vmcnt<(STAGES > 6 ? 6 : 0) * kLoads>(); break;
+    default: wait_vmcnt<(STAGES > 7 ? 7 : 0) * kLoads>(); break;
+  }
+}
 // Workgroup barrier without the compiler's memory fence; each side waits for exactly the
 // memory operations it must (the fence would drain every outstanding global load).
 __device__ __forceinline__ void barrier_lds_drained() {
@@ -262,26 +277,36 @@ __global__ __launch_bounds__((4 + NPROD) * 64, 1) void qkv_pc_kernel(QkvArgs a) 
       }
       dst_off[i] = 1024 * q;
     }
-    // Steps past the end re-read the last step into a stage nobody reads any more.
+    // Requests step kt (< nk) into `stage`. No step past the end is requested: the tail of the
+    // loop waits for fewer steps instead (re-reading the last step there, to keep one wait
+    // count, cost 1.3% at 512 rows).
     auto issue = [&](int kt, int stage) {
-      const int k0 = min(kt, nk - 1) * kKT;
+      const int k0 = kt * kKT;
       uint8_t* st = smem + stage * kStageBytes;
 #pragma unroll
       for (int i = 0; i < kLoads; ++i)
         __builtin_amdgcn_global_load_lds((glb_ptr)(src[i] + k0), (lds_ptr)(st + dst_off[i]), 16,
                                          0, 0);
     };
+    const int first = min(STAGES, nk);  // steps requested before the loop
 #pragma unroll
-    for (int s = 0; s < STAGES; ++s) issue(s, s);
-    wait_vmcnt<(STAGES - 1) * kLoads>();  // step 0 landed
+    for (int s = 0; s < STAGES; ++s)
+      if (s < first) issue(s, s);
+    wait_steps<STAGES, kLoads>(first - 1);  // step 0 landed
     barrier_only();
     int stage = 0;
-    for (int kt = 0; kt < nk; ++kt) {
+    int kt = 0;
+    for (; kt + STAGES < nk; ++kt) {
       // step kt + 1 landed (steps kt + 2 .. kt + STAGES - 1 may still be in flight)
       wait_vmcnt<(STAGES - 2) * kLoads>();
       barrier_only();
       issue(kt + STAGES, stage);  // this stage's last reads came before the barrier
       stage = stage == STAGES - 1 ? 0 : stage + 1;
+    }
+    // the last steps request nothing: step kt + 1 landed, steps kt + 2 .. nk - 1 in flight
+    for (; kt < nk; ++kt) {
+      wait_steps<STAGES, kLoads>(nk - 2 - kt);
+      barrier_only();
     }
     wait_vmcnt<0>();  // no load may still be writing LDS when the stages are reused
     barrier_only();   // -> the consumers may overwrite the stages

@@ -881,12 +881,13 @@ def test_block_attention_page_sizes(page_log2):
         _close(sc[keys], exp, atol=2e-3, rtol=1e-4, what=f"page {P}, importance seq {sq.batch}")
 
 
-@pytest.mark.parametrize("n_heads,Q", [(6, 40), (6, 300), (20, 64), (20, 700), (40, 40),
-                                       (40, 200)])
+@pytest.mark.parametrize("n_heads,Q", [(2, 40), (2, 100), (2, 300), (6, 40), (6, 300), (20, 64),
+                                       (20, 700), (40, 40), (40, 200)])
 def test_qkv_rope_cache_head_counts(n_heads, Q):
-    """Head counts 6, 20 and 40 (d_model 768-5120): tile counts that are not multiples of
-    the eight XCDs (6 heads: 36 weight-streaming tiles) and the three launch shapes, against
-    the oracle; untouched cache rows keep their contents."""
+    """Head counts 2, 6, 20 and 40 (d_model 256-5120): tile counts that are not multiples of
+    the eight XCDs (6 heads: 36 weight-streaming tiles), the three launch shapes, and
+    reductions of 4 steps, fewer than the 6 or 8 steps the weight-streaming shapes request
+    before their loop, against the oracle; untouched cache rows keep their contents."""
     rng = np.random.default_rng(100 + n_heads + Q)
     n_slots = max(1024, 2 * Q)
     slots = rng.choice(n_slots, Q, replace=False)
