@@ -1014,3 +1014,57 @@ def test_qkv_rope_halves_flag():
     _close(_np(kc), k_ref, what="k cache, halves differ")
     _close(_np(vc), v_ref, what="v cache, halves differ")
     assert not torch.equal(run(s2, c2, True)[0], q)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_verify_attention_random_blocks(seed):
+    """Seeded random Flash-Verify launches: block_m 8-128 (blocks of up to 256 rows), 1-40
+    blocks (past 256 workgroups two heads share one), one to eight heads, each block with
+    its own (T, S) (T fill rows, S drafts and S masks, fewer rows than the block holds) and a
+    key list of 0-2500 cache slots in random order; the closed-form mask in even seeds, the
+    reference's dense mask in odd ones. Against the oracle; rows outside the blocks keep their
+    contents."""
+    rng = np.random.default_rng(3000 + seed)
+    H = int(rng.choice([1, 2, 4, 8]))
+    bm = int(rng.choice([8, 16, 32, 64, 128]))
+    n_blk = int(rng.integers(1, 41))
+    if seed == 3:
+        H, n_blk = 8, 40  # 320 (block, head) pairs: two heads per workgroup
+    rows_cap = 2 * bm
+    L = 2600
+    key_pos, vblocks, masks, ts = [], [], [], []
+    acc_k = acc_q = 0
+    for _ in range(n_blk):
+        S = int(rng.integers(1, bm + 1))
+        T = int(rng.integers(0, rows_cap - 2 * S + 1))
+        nk = int(rng.integers(0, 2501))
+        keys = rng.choice(L, nk, replace=False)
+        key_pos.append(keys)
+        vblocks.append((acc_k, acc_k + nk, acc_q, acc_q + T + 2 * S))
+        acc_k += nk
+        acc_q += T + 2 * S
+        masks.append(orc.verify_mask(T, S, bm))
+        ts.append((T, S))
+    Q = acc_q + 3  # three rows past the last block stay untouched
+    key_pos = np.concatenate(key_pos).astype(np.int64)
+    vblocks = np.asarray(vblocks, np.int32)
+    mask = np.concatenate(masks)
+    lib.call("fdl_validate_vblocks", vblocks.ctypes.data, n_blk,
+             key_pos.ctypes.data if key_pos.size else None, key_pos.size, Q, L, rows_cap)
+    gen = torch.Generator().manual_seed(3100 + seed)
+    D = H * 128
+    q, k1, v1 = (_bf16((Q, D), gen) for _ in range(3))
+    kc, vc = (_bf16((L, D), gen) for _ in range(2))
+    out = torch.full((Q, D), POISON, dtype=torch.bfloat16, device=DEV)
+    meta = (torch.from_numpy(np.asarray(ts, np.int32)) if seed % 2 == 0
+            else torch.from_numpy(mask))
+    print(f"seed {seed}: H {H}, block_m {bm}, {n_blk} blocks, {key_pos.size} keys", flush=True)
+    ops.verify_attention(*(t.to(DEV) for t in (q, k1, v1, kc, vc)),
+                         torch.from_numpy(key_pos).to(DEV), torch.from_numpy(vblocks).to(DEV),
+                         meta.to(DEV), rows_cap, out, H, orc.softmax_scale(128))
+    torch.cuda.synchronize()
+    ref = orc.verify_attention(_np(q), _np(k1), _np(v1), _np(kc), _np(vc), key_pos, mask,
+                               vblocks, rows_cap, H, orc.softmax_scale(128))
+    got = _np(out)
+    _close(got[:acc_q], ref[:acc_q], what=f"verify attention, seed {seed}")
+    assert np.all(got[acc_q:] == POISON)
