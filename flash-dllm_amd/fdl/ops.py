@@ -60,7 +60,7 @@ def tables_repeat_halves(rope_sin: torch.Tensor, rope_cos: torch.Tensor) -> bool
     if (hit is not None and hit[0]() is rope_sin and hit[1]() is rope_cos
             and hit[2] == (rope_sin._version, rope_cos._version)):
         return hit[3]
-    if torch.cuda.is_current_stream_capturing():
+    if rope_sin.is_cuda and torch.cuda.is_current_stream_capturing():
         return False
     h = rope_sin.shape[1] // 2
     same = bool(rope_sin.shape[1] % 2 == 0
