@@ -169,8 +169,10 @@ struct EpGroup {
                        pack_bf16x2(r[6], r[7])};
     uint16_t* base = mat == 0 ? a.q_out : (mat == 1 ? a.k_out : a.v_out);
     uint16_t* d = base + dst * a.d_model + int64_t(head) * kHeadDim + c0;
-    st16(d, wlo);
-    st16(d + kHalf, whi);
+    // non-temporal: the whole grid writes its Q/K/V rows at once at the end (1.5% faster at
+    // 512 rows, 2% at 6842; the attention that reads them next is unchanged)
+    __builtin_nontemporal_store(wlo, reinterpret_cast<u32x4*>(d));
+    __builtin_nontemporal_store(whi, reinterpret_cast<u32x4*>(d + kHalf));
   }
 };
 
